@@ -1,0 +1,168 @@
+// Shared definitions of libitts_hip: device-side weight descriptors, decode control
+// block, number-format helpers and wavefront reductions for gfx950 (wave64).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace itts {
+
+constexpr int kHeadDim = 64;
+constexpr int kGroup = 64;
+constexpr int kSeenWords = 129;  // SeenTokenBitSet: 129 u64 words cover ids 0..8255
+
+enum ParamType : int { kParamF16 = 0, kParamF32 = 1 };
+enum KvType : int { kKvBf16 = 0, kKvF32 = 1 };
+
+// One QuantizedLinear as stored on the device.
+//   codes : bits=8 uint8 [N][K]; bits=4 uint8 [N][K/2] (low nibble = even k)
+//   params: per (row, 64-group) the pair (scale, bias): fp16x2 packed in a uint32
+//           (scale in the low half) or float2, [N][K/64]
+//   bias  : fp32 [N]
+struct DevQL {
+  const uint8_t *codes;
+  const void *params;
+  const float *bias;
+  int N, K;
+};
+
+struct DevLayer {
+  const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;
+  DevQL attn, proj, fc, mproj;
+};
+
+// Per-sequence decode state kept in device memory so that one captured step can be
+// replayed for every token: the kernels read the token, its position and the cache
+// length from here, and the sampler writes the next ones.
+struct DecodeCtl {
+  int32_t tok;        // Mel token fed to the next step
+  int32_t pos;        // its Mel position index
+  int32_t valid_len;  // KV rows written before the next step
+  int32_t done;       // generation finished (STOP sampled or max_steps reached)
+  int32_t n_codes;    // codes emitted so far
+  int32_t step;       // sampling step index s
+  int32_t min_codes;
+  int32_t max_steps;
+  int32_t n_prior;
+  int32_t last_tok;   // last sampled token (STOP included)
+  uint64_t rng;       // SamplerRng state
+  uint64_t seen[kSeenWords];
+};
+
+// Sampling parameters as the device sampler consumes them.
+struct DevSampling {
+  int32_t greedy;
+  float inv_temp;     // 1 / temperature, rounded once on the host
+  float top_p;
+  int32_t top_k;      // effective k (1..n)
+  float penalty;
+  int32_t apply_penalty;
+};
+
+__host__ __device__ inline uint32_t next_pow2(uint32_t v) {
+  uint32_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+__device__ inline float half_bits_to_float(uint32_t h) {
+  return __half2float(__ushort_as_half((unsigned short)h));
+}
+
+__device__ inline float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ inline uint32_t float_to_bf16_bits(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (x >> 16) | 0x40u;
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return x >> 16;
+}
+
+// (scale, bias) of one (row, group).
+template <int PT>
+__device__ inline float2 load_param(const void *params, size_t idx) {
+  if constexpr (PT == kParamF16) {
+    const uint32_t w = static_cast<const uint32_t *>(params)[idx];
+    return make_float2(half_bits_to_float(w & 0xffffu), half_bits_to_float(w >> 16));
+  } else {
+    return static_cast<const float2 *>(params)[idx];
+  }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// gelu_approximate (tanh form).
+__device__ inline float gelu_tanh(float x) {
+  const float x3 = x * x * x;
+  const float inner = 0.7978845608028654f * (x + 0.044715f * x3);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// Sum over a block of NT threads; every thread receives the same value, formed in the
+// same order on every block (deterministic).
+template <int NT>
+__device__ inline float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NT / 64; i++) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// LayerNorm of x[n] (global) into xl[n] (LDS): biased variance, eps 1e-5.
+template <int NT>
+__device__ inline void layernorm_to_lds(const float *x, const float *w, const float *b, int n,
+                                        float *xl, float *red) {
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const float v = x[i];
+    xl[i] = v;
+    s += v;
+  }
+  const float mean = block_sum<NT>(s, red) / (float)n;
+  float q = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const float d = xl[i] - mean;
+    q += d * d;
+  }
+  const float var = block_sum<NT>(q, red) / (float)n;
+  const float rstd = 1.0f / sqrtf(var + 1e-5f);
+  for (int i = threadIdx.x; i < n; i += NT) xl[i] = (xl[i] - mean) * rstd * w[i] + b[i];
+  __syncthreads();
+}
+
+// Same, in place on an LDS row.
+template <int NT>
+__device__ inline void layernorm_lds_inplace(float *xl, const float *w, const float *b, int n,
+                                             float *red) {
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) s += xl[i];
+  const float mean = block_sum<NT>(s, red) / (float)n;
+  float q = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const float d = xl[i] - mean;
+    q += d * d;
+  }
+  const float var = block_sum<NT>(q, red) / (float)n;
+  const float rstd = 1.0f / sqrtf(var + 1e-5f);
+  for (int i = threadIdx.x; i < n; i += NT) xl[i] = (xl[i] - mean) * rstd * w[i] + b[i];
+  __syncthreads();
+}
+
+}  // namespace itts

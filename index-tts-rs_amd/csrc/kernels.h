@@ -1,0 +1,92 @@
+// Host-side launchers of the gfx950 kernels.  Every launcher enqueues on `stream` and
+// returns the launch status; shapes are validated by the caller (runtime.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace itts {
+
+enum Prologue : int { kProNone = 0, kProLN = 1, kProLNLN = 2 };
+enum Epilogue : int { kEpiStore = 0, kEpiResid = 1, kEpiGelu = 2, kEpiQKV = 3 };
+
+// Where the QKV epilogue scatters: q -> q_out[M][d]; k, v -> this layer's cache
+// [n_head][max_seq][64] at rows pos0.. (pos0 = ctl->valid_len when ctl != nullptr).
+struct QkvDst {
+  float *q_out;
+  void *k_cache;
+  void *v_cache;
+  int max_seq;
+  int pos0;
+  int d_model;
+};
+
+struct GemvArgs {
+  DevQL ql;
+  const float *x;          // input row [K]
+  const float *ln_w, *ln_b;    // LN (prologue kProLN / first LN of kProLNLN)
+  const float *ln2_w, *ln2_b;  // second LN of kProLNLN
+  float *y;                // output row [N] (store / gelu) or residual stream (resid)
+  QkvDst qkv;
+  const DecodeCtl *ctl;    // optional: early exit when done, cache row = valid_len
+};
+
+hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi, int kvt,
+                       hipStream_t s);
+
+// Decode attention: q [n_head*64] against cache rows 0..valid_len (inclusive of the
+// row the step just wrote), split over the keys; then the split combine.
+hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, int n_head,
+                              int max_seq, const DecodeCtl *ctl, int static_len, float *part,
+                              int max_splits, int chunk, float *out, int kvt, hipStream_t s);
+
+// Causal attention of T rows at cache positions base..base+T-1 (prefill).
+hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
+                               int n_head, int max_seq, float *out, int kvt, hipStream_t s);
+
+// x = mel_emb[ctl->tok] + mel_pos[ctl->pos]  (or the given tok/pos when ctl == nullptr)
+hipError_t launch_embed_step(const float *mel_emb, const float *mel_pos, const DecodeCtl *ctl,
+                             int d, float *x, hipStream_t s);
+
+// Row descriptors for the prefill embedding.
+struct EmbedRow {
+  int kind;  // 0 cond row, 1 text row, 2 Mel row
+  int id;    // cond row index / token id
+  int pos;   // positional index
+};
+hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
+                             const float *text_emb, const float *lang_row,
+                             const float *text_pos, const float *mel_emb,
+                             const float *mel_pos, int d, float *x, hipStream_t s);
+
+// LN of T rows [T][d] -> [T][d].
+hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
+                          float *y, hipStream_t s);
+
+// Prefill GEMM: y = x[M][K] . Wdeq^T + bias with the same epilogues as the GEMV.
+struct GemmArgs {
+  DevQL ql;
+  const float *x;   // [M][K]
+  int M;
+  float *y;         // [M][N] (store / gelu) or residual stream [M][N] (resid)
+  QkvDst qkv;
+};
+hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s);
+
+hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipStream_t s);
+
+// Device sampler (one block).  mode 0: API call on `logits` (penalised in place,
+// token to *tok_out, rng advanced); mode 1: generate step driven by ctl.
+// Raises the sampler's dynamic-LDS limit; call once per process before any launch
+// (never during stream capture).
+hipError_t sampler_init();
+
+hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSampling p,
+                          uint64_t *rng, int32_t *tok_out, DecodeCtl *ctl, int32_t *codes,
+                          int stop_tok, int mode, hipStream_t s);
+
+// ctl->valid_len += 1 after a decode step (skipped when done).
+hipError_t launch_step_finish(DecodeCtl *ctl, hipStream_t s);
+
+}  // namespace itts

@@ -1,0 +1,1000 @@
+// libitts_hip runtime: the C ABI of include/itts_hip.h over the gfx950 kernels.
+//
+// Mirrors the reference's decoder interface (crates/core/src/models/gpt.rs and
+// sampler.rs): Gpt::from_weights -> itts_gpt_create, KvCache::new -> itts_kv_create,
+// prefill / prefill_after / step, sample_next_token and generate_codes_after.
+// Everything here is host orchestration; all arithmetic runs in the HIP kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/itts_hip.h"
+#include "kernels.h"
+
+using namespace itts;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+itts_status set_error(itts_status st, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+#define HIP_TRY(expr)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return set_error(ITTS_E_DEVICE, "HIP error %s at %s:%d: %s", hipGetErrorName(e_), \
+                       __FILE__, __LINE__, #expr);                                       \
+  } while (0)
+
+constexpr int kAttnChunk = 64;  // keys per decode-attention split
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  hipError_t ensure(size_t n) {
+    if (n <= bytes) return hipSuccess;
+    if (p) {
+      hipError_t e = hipFree(p);
+      if (e != hipSuccess) return e;
+      p = nullptr;
+      bytes = 0;
+    }
+    hipError_t e = hipMalloc(&p, n);
+    if (e == hipSuccess) bytes = n;
+    return e;
+  }
+  template <class T>
+  T *as() const {
+    return static_cast<T *>(p);
+  }
+};
+
+bool valid_config(const itts_config &c, std::string &why) {
+  char b[256];
+  auto fail = [&](const char *m) {
+    why = m;
+    return false;
+  };
+  if (c.n_layer <= 0) return fail("config: n_layer must be >= 1");
+  if (c.n_head <= 0 || c.d_model != c.n_head * 64) return fail("config: d_model must equal n_head * 64");
+  if (c.d_ffn <= 0 || c.d_ffn % 64 != 0) return fail("config: d_ffn must be a positive multiple of 64");
+  if (c.quant_bits != 8 && c.quant_bits != 4) return fail("config: quant_bits must be 8 or 4");
+  if (c.param_dtype != ITTS_F16 && c.param_dtype != ITTS_F32) return fail("config: param_dtype must be F16 or F32");
+  const int epc = c.quant_bits == 8 ? 16 : 32;
+  if (c.d_model / epc > 512 || c.d_ffn / epc > 512) return fail("config: K too large for the decode GEMV");
+  if (c.mel_vocab < 3 || c.mel_vocab > 9216) return fail("config: mel_vocab must be in 3..=9216");
+  if (c.text_vocab < 2 || c.lang_vocab < 1) return fail("config: text_vocab >= 2 and lang_vocab >= 1");
+  if (c.mel_pos_len < 3 || c.text_pos_len < 3) return fail("config: positional tables too short");
+  (void)b;
+  return true;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------
+// Handles
+// ------------------------------------------------------------------------------------
+
+struct QLHost {
+  DevBuf codes, params, bias;
+  DevQL dev() const { return DevQL{codes.as<uint8_t>(), params.p, bias.as<float>(), N, K}; }
+  int N = 0, K = 0;
+};
+
+struct itts_gpt {
+  itts_config cfg{};
+  hipStream_t stream = nullptr;
+  int max_cond = 64;
+  DevBuf text_emb, lang_emb, mel_emb, mel_pos, text_pos;
+  std::vector<DevBuf> ln;  // ln1_w, ln1_b, ln2_w, ln2_b per layer, then ln_f, final_norm
+  std::vector<QLHost> qls; // 4 per layer, then mel_head
+  std::vector<DevLayer> layers;
+  DevBuf ln_f_w, ln_f_b, fn_w, fn_b;
+  DevQL head{};
+  // decode workspace
+  DevBuf x, q, a, f, logits;
+  // prefill workspace (grown on demand)
+  DevBuf px, ph, pq, pa, pf, rows, conds;
+  // sampler API scratch
+  DevBuf s_logits, s_seen, s_rng, s_tok;
+  int ptype() const { return cfg.param_dtype == ITTS_F32 ? kParamF32 : kParamF16; }
+};
+
+struct itts_kv {
+  itts_gpt *gpt = nullptr;
+  int max_seq = 0;
+  int kvt = kKvBf16;
+  int valid_len = 0;
+  DevBuf k, v;         // [n_layer][n_head][max_seq][64]
+  DevBuf ctl;          // DecodeCtl
+  DevBuf part;         // attention split partials [n_head][splits][66]
+  DevBuf codes;        // generate output
+  DecodeCtl *host_ctl = nullptr;  // pinned staging, 2 slots
+  int splits = 0;
+  // captured decode iteration (sampler + step), keyed by the sampling parameters
+  hipGraphExec_t gexec = nullptr;
+  hipGraph_t graph = nullptr;
+  DevSampling gkey{};
+  bool have_graph = false;
+  size_t layer_elems() const { return (size_t)gpt->cfg.n_head * max_seq * 64; }
+  void *k_layer(int l) const {
+    return static_cast<char *>(k.p) + layer_elems() * l * (kvt == kKvBf16 ? 2 : 4);
+  }
+  void *v_layer(int l) const {
+    return static_cast<char *>(v.p) + layer_elems() * l * (kvt == kKvBf16 ? 2 : 4);
+  }
+  ~itts_kv() {
+    if (gexec) (void)hipGraphExecDestroy(gexec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (host_ctl) (void)hipHostFree(host_ctl);
+  }
+};
+
+namespace {
+
+hipError_t upload(DevBuf &b, const void *src, size_t bytes) {
+  hipError_t e = b.ensure(bytes);
+  if (e != hipSuccess) return e;
+  return hipMemcpy(b.p, src, bytes, hipMemcpyHostToDevice);
+}
+
+// Packs scales/biases [N][G] into the device's interleaved (scale, bias) pairs.
+std::vector<uint8_t> pack_params(const void *scales, const void *biases, size_t count, bool f32) {
+  std::vector<uint8_t> out(count * (f32 ? 8 : 4));
+  if (f32) {
+    const float *s = static_cast<const float *>(scales), *b = static_cast<const float *>(biases);
+    float *o = reinterpret_cast<float *>(out.data());
+    for (size_t i = 0; i < count; i++) {
+      o[2 * i] = s[i];
+      o[2 * i + 1] = b[i];
+    }
+  } else {
+    const uint16_t *s = static_cast<const uint16_t *>(scales), *b = static_cast<const uint16_t *>(biases);
+    uint32_t *o = reinterpret_cast<uint32_t *>(out.data());
+    for (size_t i = 0; i < count; i++) o[i] = (uint32_t)s[i] | ((uint32_t)b[i] << 16);
+  }
+  return out;
+}
+
+itts_status upload_ql(QLHost &dst, const itts_qlinear &src, int N, int K, int bits, bool f32,
+                      const char *name) {
+  if (!src.codes || !src.scales || !src.biases || !src.bias)
+    return set_error(ITTS_E_WEIGHT, "weight load error in `%s`: missing tensor", name);
+  dst.N = N;
+  dst.K = K;
+  const size_t G = (size_t)K / 64;
+  HIP_TRY(upload(dst.codes, src.codes, (size_t)N * K * bits / 8));
+  std::vector<uint8_t> pk = pack_params(src.scales, src.biases, (size_t)N * G, f32);
+  HIP_TRY(upload(dst.params, pk.data(), pk.size()));
+  HIP_TRY(upload(dst.bias, src.bias, sizeof(float) * N));
+  return ITTS_OK;
+}
+
+itts_status check_vec(const float *p, const char *name) {
+  if (!p) return set_error(ITTS_E_WEIGHT, "weight load error in `%s`: missing tensor", name);
+  return ITTS_OK;
+}
+
+DevSampling to_dev_sampling(const itts_sampling &p, int n) {
+  DevSampling d{};
+  d.greedy = p.greedy ? 1 : 0;
+  d.inv_temp = 1.0f / p.temperature;
+  d.top_p = p.top_p;
+  d.top_k = p.top_k == 0 ? n : std::min<int>((int)p.top_k, n);
+  d.penalty = p.repetition_penalty;
+  d.apply_penalty = std::fabs(p.repetition_penalty - 1.0f) <= 1.1920928955078125e-7f ? 0 : 1;
+  return d;
+}
+
+// Enqueues the stack over the rows already embedded in gpt->px (prefill, T rows at
+// cache positions 0..T-1) and the head of the last row into gpt->logits.
+itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model, F = c.d_ffn, bits = c.quant_bits, pt = g->ptype();
+  hipStream_t s = g->stream;
+  float *X = g->px.as<float>(), *Hn = g->ph.as<float>(), *Q = g->pq.as<float>();
+  float *A = g->pa.as<float>(), *Fb = g->pf.as<float>();
+  for (int l = 0; l < c.n_layer; l++) {
+    const DevLayer &L = g->layers[l];
+    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, Hn, s));
+    GemmArgs ga{};
+    ga.ql = L.attn;
+    ga.x = Hn;
+    ga.M = T;
+    ga.qkv = QkvDst{Q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kv->kvt, s));
+    HIP_TRY(launch_attn_prefill(Q, T, 0, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, A,
+                                kv->kvt, s));
+    ga = GemmArgs{};
+    ga.ql = L.proj;
+    ga.x = A;
+    ga.M = T;
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
+    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, T, d, Hn, s));
+    ga = GemmArgs{};
+    ga.ql = L.fc;
+    ga.x = Hn;
+    ga.M = T;
+    ga.y = Fb;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kv->kvt, s));
+    ga = GemmArgs{};
+    ga.ql = L.mproj;
+    ga.x = Fb;
+    ga.M = T;
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
+  }
+  (void)F;
+  GemvArgs ha{};
+  ha.ql = g->head;
+  ha.x = X + (size_t)(T - 1) * d;
+  ha.ln_w = g->ln_f_w.as<float>();
+  ha.ln_b = g->ln_f_b.as<float>();
+  ha.ln2_w = g->fn_w.as<float>();
+  ha.ln2_b = g->fn_b.as<float>();
+  ha.y = g->logits.as<float>();
+  HIP_TRY(launch_gemv(ha, bits, pt, kProLNLN, kEpiStore, kv->kvt, s));
+  return ITTS_OK;
+}
+
+// Enqueues one decode step driven by kv->ctl (token, position and cache length read on
+// the device): logits land in gpt->logits and ctl->valid_len advances.
+itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
+  hipStream_t s = g->stream;
+  DecodeCtl *ctl = kv->ctl.as<DecodeCtl>();
+  float *x = g->x.as<float>(), *q = g->q.as<float>(), *a = g->a.as<float>(), *f = g->f.as<float>();
+  HIP_TRY(launch_embed_step(g->mel_emb.as<float>(), g->mel_pos.as<float>(), ctl, d, x, s));
+  for (int l = 0; l < c.n_layer; l++) {
+    const DevLayer &L = g->layers[l];
+    GemvArgs ga{};
+    ga.ql = L.attn;
+    ga.x = x;
+    ga.ln_w = L.ln1_w;
+    ga.ln_b = L.ln1_b;
+    ga.qkv = QkvDst{q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
+    ga.ctl = ctl;
+    HIP_TRY(launch_gemv(ga, bits, pt, kProLN, kEpiQKV, kv->kvt, s));
+    HIP_TRY(launch_attn_decode(q, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, ctl, 0,
+                               kv->part.as<float>(), kv->splits, kAttnChunk, a, kv->kvt, s));
+    ga = GemvArgs{};
+    ga.ql = L.proj;
+    ga.x = a;
+    ga.y = x;
+    ga.ctl = ctl;
+    HIP_TRY(launch_gemv(ga, bits, pt, kProNone, kEpiResid, kv->kvt, s));
+    ga = GemvArgs{};
+    ga.ql = L.fc;
+    ga.x = x;
+    ga.ln_w = L.ln2_w;
+    ga.ln_b = L.ln2_b;
+    ga.y = f;
+    ga.ctl = ctl;
+    HIP_TRY(launch_gemv(ga, bits, pt, kProLN, kEpiGelu, kv->kvt, s));
+    ga = GemvArgs{};
+    ga.ql = L.mproj;
+    ga.x = f;
+    ga.y = x;
+    ga.ctl = ctl;
+    HIP_TRY(launch_gemv(ga, bits, pt, kProNone, kEpiResid, kv->kvt, s));
+  }
+  GemvArgs ha{};
+  ha.ql = g->head;
+  ha.x = x;
+  ha.ln_w = g->ln_f_w.as<float>();
+  ha.ln_b = g->ln_f_b.as<float>();
+  ha.ln2_w = g->fn_w.as<float>();
+  ha.ln2_b = g->fn_b.as<float>();
+  ha.y = g->logits.as<float>();
+  ha.ctl = ctl;
+  HIP_TRY(launch_gemv(ha, bits, pt, kProLNLN, kEpiStore, kv->kvt, s));
+  HIP_TRY(launch_step_finish(ctl, s));
+  return ITTS_OK;
+}
+
+itts_status validate_prefix(const itts_config &c, const int32_t *text, int32_t n_text,
+                            const float *conds, int32_t n_cond, int32_t max_cond, int32_t lang,
+                            const int32_t *prior, int32_t n_prior) {
+  // gpt.rs:536-560 (prefix_embedding) and 605-613 (sequence_embedding), in that order
+  if (n_prior < 0 || n_prior + 3 > c.mel_pos_len)
+    return set_error(ITTS_E_VALIDATION, "codes: %d codes exceed the Mel positional capacity", n_prior);
+  if (n_text <= 0 || !text) return set_error(ITTS_E_VALIDATION, "text_tokens: text_tokens must not be empty");
+  if (n_text + 2 > c.text_pos_len)
+    return set_error(ITTS_E_VALIDATION, "text_tokens: text sequence length %d exceeds %d", n_text + 2,
+                     c.text_pos_len);
+  if (n_cond < 0 || n_cond > max_cond || (n_cond > 0 && !conds))
+    return set_error(ITTS_E_VALIDATION, "conds: expected 0..=%d rows of %d, got %d", max_cond, c.d_model,
+                     n_cond);
+  if (lang < 0 || lang >= c.lang_vocab)
+    return set_error(ITTS_E_VALIDATION, "lang_id: lang_id %d out of range 0..%d", lang, c.lang_vocab);
+  for (int i = 0; i < n_text; i++)
+    if (text[i] < 0 || text[i] >= c.text_vocab)
+      return set_error(ITTS_E_VALIDATION, "text_tokens: id %d out of range 0..%d", text[i], c.text_vocab);
+  if (n_prior > 0 && !prior) return set_error(ITTS_E_VALIDATION, "codes: null prior codes");
+  for (int i = 0; i < n_prior; i++)
+    if (prior[i] < 0 || prior[i] >= c.mel_vocab)
+      return set_error(ITTS_E_VALIDATION, "codes: id %d out of range 0..%d", prior[i], c.mel_vocab);
+  return ITTS_OK;
+}
+
+// Embeds the prefill rows into gpt->px and runs the stack; on success the cache holds T
+// rows and gpt->logits the next-token logits.  The cache is reset first (gpt.rs:664).
+itts_status run_prefill(itts_gpt *g, itts_kv *kv, const int32_t *text, int32_t n_text,
+                        const float *conds, int32_t n_cond, int32_t lang, const int32_t *prior,
+                        int32_t n_prior, int *T_out) {
+  const itts_config &c = g->cfg;
+  itts_status st = validate_prefix(c, text, n_text, conds, n_cond, g->max_cond, lang, prior, n_prior);
+  if (st) return st;
+  const int d = c.d_model;
+  const int T = n_cond + n_text + 3 + n_prior;
+  kv->valid_len = 0;
+  if (T > kv->max_seq)
+    return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d", T,
+                     kv->max_seq);
+  std::vector<EmbedRow> rows;
+  rows.reserve(T);
+  for (int i = 0; i < n_cond; i++) rows.push_back({0, i, 0});
+  for (int j = 0; j < n_text + 2; j++) {
+    const int u = j == 0 ? 0 : (j == n_text + 1 ? 1 : text[j - 1]);
+    rows.push_back({1, u, j});
+  }
+  rows.push_back({2, c.mel_vocab - 2, 0});
+  for (int i = 0; i < n_prior; i++) rows.push_back({2, prior[i], i + 2});
+  HIP_TRY(g->px.ensure(sizeof(float) * (size_t)T * d));
+  HIP_TRY(g->ph.ensure(sizeof(float) * (size_t)T * d));
+  HIP_TRY(g->pq.ensure(sizeof(float) * (size_t)T * d));
+  HIP_TRY(g->pa.ensure(sizeof(float) * (size_t)T * d));
+  HIP_TRY(g->pf.ensure(sizeof(float) * (size_t)T * c.d_ffn));
+  HIP_TRY(g->rows.ensure(sizeof(EmbedRow) * (size_t)T));
+  HIP_TRY(g->conds.ensure(sizeof(float) * (size_t)std::max(1, n_cond) * d));
+  HIP_TRY(hipMemcpyAsync(g->rows.p, rows.data(), sizeof(EmbedRow) * T, hipMemcpyHostToDevice, g->stream));
+  if (n_cond > 0)
+    HIP_TRY(hipMemcpyAsync(g->conds.p, conds, sizeof(float) * (size_t)n_cond * d, hipMemcpyHostToDevice,
+                           g->stream));
+  HIP_TRY(launch_embed_rows(g->rows.as<EmbedRow>(), T, g->conds.as<float>(), g->text_emb.as<float>(),
+                            g->lang_emb.as<float>() + (size_t)lang * d, g->text_pos.as<float>(),
+                            g->mel_emb.as<float>(), g->mel_pos.as<float>(), d, g->px.as<float>(),
+                            g->stream));
+  st = enqueue_prefill_stack(g, kv, T);
+  if (st) return st;
+  kv->valid_len = T;
+  *T_out = T;
+  return ITTS_OK;
+}
+
+// Writes the host-known fields of the decode control block.
+itts_status write_ctl(itts_kv *kv, const DecodeCtl &h) {
+  *kv->host_ctl = h;
+  HIP_TRY(hipMemcpyAsync(kv->ctl.p, kv->host_ctl, sizeof(DecodeCtl), hipMemcpyHostToDevice,
+                         kv->gpt->stream));
+  return ITTS_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------
+// C ABI
+// ------------------------------------------------------------------------------------
+
+extern "C" {
+
+const char *itts_version(void) { return "libitts_hip 0.1.0 (gfx950)"; }
+
+const char *itts_last_error(void) { return g_last_error.c_str(); }
+
+itts_config itts_config_default(void) {
+  itts_config c{};
+  c.n_layer = 24;
+  c.d_model = 1280;
+  c.n_head = 20;
+  c.d_ffn = 5120;
+  c.mel_vocab = 8194;
+  c.text_vocab = 60510;
+  c.lang_vocab = 107;
+  c.mel_pos_len = 1818;
+  c.text_pos_len = 602;
+  c.quant_bits = 8;
+  c.param_dtype = ITTS_F16;
+  return c;
+}
+
+itts_sampling itts_sampling_default(void) {
+  itts_sampling p{};
+  p.greedy = 0;
+  p.temperature = 0.8f;
+  p.top_p = 0.8f;
+  p.top_k = 3;
+  p.repetition_penalty = 10.0f;
+  p.max_mel_tokens = 1500;
+  return p;
+}
+
+itts_status itts_sampling_validate(const itts_sampling *p) {
+  if (!p) return set_error(ITTS_E_VALIDATION, "sampling: null");
+  if (!std::isfinite(p->temperature) || !(p->temperature >= 0.05f && p->temperature <= 2.0f))
+    return set_error(ITTS_E_VALIDATION, "temperature: must be finite and in 0.05..=2.0, got %g",
+                     (double)p->temperature);
+  if (!std::isfinite(p->top_p) || !(p->top_p >= 0.01f && p->top_p <= 1.0f))
+    return set_error(ITTS_E_VALIDATION, "top_p: must be finite and in 0.01..=1.0, got %g", (double)p->top_p);
+  if (p->top_k > 8194) return set_error(ITTS_E_VALIDATION, "top_k: must be <= 8194, got %u", p->top_k);
+  if (!std::isfinite(p->repetition_penalty) ||
+      !(p->repetition_penalty >= 1.0f && p->repetition_penalty <= 50.0f))
+    return set_error(ITTS_E_VALIDATION, "repetition_penalty: must be finite and in 1.0..=50.0, got %g",
+                     (double)p->repetition_penalty);
+  if (p->max_mel_tokens < 1 || p->max_mel_tokens > 1815)
+    return set_error(ITTS_E_VALIDATION, "max_mel_tokens: must be in 1..=1815, got %u", p->max_mel_tokens);
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
+  if (!w || !out) return set_error(ITTS_E_VALIDATION, "weights: null argument");
+  std::string why;
+  if (!valid_config(w->config, why)) return set_error(ITTS_E_WEIGHT, "weight load error in `config`: %s", why.c_str());
+  auto *g = new itts_gpt();
+  g->cfg = w->config;
+  const itts_config &c = g->cfg;
+  const int d = c.d_model, F = c.d_ffn, bits = c.quant_bits;
+  const bool f32 = c.param_dtype == ITTS_F32;
+  auto fail = [&](itts_status st) {
+    delete g;
+    return st;
+  };
+  if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess)
+    return fail(set_error(ITTS_E_DEVICE, "hipStreamCreate failed"));
+  if (sampler_init() != hipSuccess) return fail(set_error(ITTS_E_DEVICE, "sampler LDS attribute failed"));
+  struct {
+    const float *p;
+    const char *name;
+    DevBuf *dst;
+    size_t n;
+  } tabs[] = {
+      {w->text_embedding, "text_embedding.weight", &g->text_emb, (size_t)c.text_vocab * d},
+      {w->lang_embedding, "lang_embedding.weight", &g->lang_emb, (size_t)c.lang_vocab * d},
+      {w->mel_embedding, "mel_embedding.weight", &g->mel_emb, (size_t)c.mel_vocab * d},
+      {w->mel_pos_embedding, "mel_pos_embedding.emb.weight", &g->mel_pos, (size_t)c.mel_pos_len * d},
+      {w->text_pos_embedding, "text_pos_embedding.emb.weight", &g->text_pos, (size_t)c.text_pos_len * d},
+      {w->ln_f_w, "gpt.ln_f.weight", &g->ln_f_w, (size_t)d},
+      {w->ln_f_b, "gpt.ln_f.bias", &g->ln_f_b, (size_t)d},
+      {w->final_norm_w, "final_norm.weight", &g->fn_w, (size_t)d},
+      {w->final_norm_b, "final_norm.bias", &g->fn_b, (size_t)d},
+  };
+  for (auto &t : tabs) {
+    if (itts_status st = check_vec(t.p, t.name)) return fail(st);
+    if (upload(*t.dst, t.p, sizeof(float) * t.n) != hipSuccess)
+      return fail(set_error(ITTS_E_DEVICE, "upload of `%s` failed", t.name));
+  }
+  if (!w->layers) return fail(set_error(ITTS_E_WEIGHT, "weight load error in `gpt.h`: missing layers"));
+  g->ln.resize((size_t)c.n_layer * 4);
+  g->qls.resize((size_t)c.n_layer * 4 + 1);
+  g->layers.resize(c.n_layer);
+  char name[128];
+  for (int l = 0; l < c.n_layer; l++) {
+    const itts_layer_weights &L = w->layers[l];
+    const float *lnp[4] = {L.ln1_w, L.ln1_b, L.ln2_w, L.ln2_b};
+    const char *lnn[4] = {"ln_1.weight", "ln_1.bias", "ln_2.weight", "ln_2.bias"};
+    for (int i = 0; i < 4; i++) {
+      snprintf(name, sizeof name, "gpt.h.%d.%s", l, lnn[i]);
+      if (itts_status st = check_vec(lnp[i], name)) return fail(st);
+      if (upload(g->ln[l * 4 + i], lnp[i], sizeof(float) * d) != hipSuccess)
+        return fail(set_error(ITTS_E_DEVICE, "upload of `%s` failed", name));
+    }
+    const itts_qlinear *qs[4] = {&L.c_attn, &L.c_proj, &L.c_fc, &L.mlp_c_proj};
+    const int Ns[4] = {3 * d, d, F, d}, Ks[4] = {d, d, d, F};
+    const char *qn[4] = {"attn.c_attn", "attn.c_proj", "mlp.c_fc", "mlp.c_proj"};
+    for (int i = 0; i < 4; i++) {
+      snprintf(name, sizeof name, "gpt.h.%d.%s", l, qn[i]);
+      if (itts_status st = upload_ql(g->qls[l * 4 + i], *qs[i], Ns[i], Ks[i], bits, f32, name)) return fail(st);
+    }
+    DevLayer &D = g->layers[l];
+    D.ln1_w = g->ln[l * 4].as<float>();
+    D.ln1_b = g->ln[l * 4 + 1].as<float>();
+    D.ln2_w = g->ln[l * 4 + 2].as<float>();
+    D.ln2_b = g->ln[l * 4 + 3].as<float>();
+    D.attn = g->qls[l * 4].dev();
+    D.proj = g->qls[l * 4 + 1].dev();
+    D.fc = g->qls[l * 4 + 2].dev();
+    D.mproj = g->qls[l * 4 + 3].dev();
+  }
+  QLHost &hq = g->qls[(size_t)c.n_layer * 4];
+  if (itts_status st = upload_ql(hq, w->mel_head, c.mel_vocab, d, bits, f32, "mel_head")) return fail(st);
+  g->head = hq.dev();
+  if (g->x.ensure(sizeof(float) * d) || g->q.ensure(sizeof(float) * d) || g->a.ensure(sizeof(float) * d) ||
+      g->f.ensure(sizeof(float) * F) || g->logits.ensure(sizeof(float) * c.mel_vocab))
+    return fail(set_error(ITTS_E_DEVICE, "workspace allocation failed"));
+  *out = g;
+  return ITTS_OK;
+}
+
+void itts_gpt_destroy(itts_gpt *gpt) {
+  if (!gpt) return;
+  if (gpt->stream) {
+    (void)hipStreamSynchronize(gpt->stream);
+    (void)hipStreamDestroy(gpt->stream);
+  }
+  delete gpt;
+}
+
+int32_t itts_gpt_num_layers(const itts_gpt *gpt) { return gpt ? gpt->cfg.n_layer : 0; }
+int32_t itts_gpt_max_cond(const itts_gpt *gpt) { return gpt ? gpt->max_cond : 0; }
+void *itts_gpt_stream(const itts_gpt *gpt) { return gpt ? (void *)gpt->stream : nullptr; }
+
+itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, itts_kv **out) {
+  if (!gpt || !out) return set_error(ITTS_E_VALIDATION, "kv_cache: null argument");
+  if (max_seq <= 0) return set_error(ITTS_E_VALIDATION, "max_seq: KV cache max_seq must be >= 1");
+  if (kv_dtype != ITTS_BF16 && kv_dtype != ITTS_F32)
+    return set_error(ITTS_E_VALIDATION, "kv_dtype: must be BF16 or F32");
+  auto *kv = new itts_kv();
+  kv->gpt = gpt;
+  kv->max_seq = max_seq;
+  kv->kvt = kv_dtype == ITTS_BF16 ? kKvBf16 : kKvF32;
+  const size_t es = kv->kvt == kKvBf16 ? 2 : 4;
+  const size_t n = (size_t)gpt->cfg.n_layer * kv->layer_elems();
+  kv->splits = (max_seq + kAttnChunk - 1) / kAttnChunk;
+  if (kv->k.ensure(n * es) || kv->v.ensure(n * es) || kv->ctl.ensure(sizeof(DecodeCtl)) ||
+      kv->part.ensure(sizeof(float) * (size_t)gpt->cfg.n_head * kv->splits * 66) ||
+      kv->codes.ensure(sizeof(int32_t) * 2048) ||
+      hipHostMalloc((void **)&kv->host_ctl, 2 * sizeof(DecodeCtl), hipHostMallocDefault) != hipSuccess) {
+    delete kv;
+    return set_error(ITTS_E_DEVICE, "KV cache allocation of %zu bytes failed", 2 * n * es);
+  }
+  if (hipMemsetAsync(kv->k.p, 0, n * es, gpt->stream) != hipSuccess ||
+      hipMemsetAsync(kv->v.p, 0, n * es, gpt->stream) != hipSuccess ||
+      hipStreamSynchronize(gpt->stream) != hipSuccess) {
+    delete kv;
+    return set_error(ITTS_E_DEVICE, "KV cache initialisation failed");
+  }
+  *out = kv;
+  return ITTS_OK;
+}
+
+void itts_kv_destroy(itts_kv *kv) {
+  if (!kv) return;
+  if (kv->gpt && kv->gpt->stream) (void)hipStreamSynchronize(kv->gpt->stream);
+  delete kv;
+}
+
+void itts_kv_reset(itts_kv *kv) {
+  if (kv) kv->valid_len = 0;
+}
+int32_t itts_kv_valid_len(const itts_kv *kv) { return kv ? kv->valid_len : 0; }
+int32_t itts_kv_max_seq(const itts_kv *kv) { return kv ? kv->max_seq : 0; }
+
+itts_status itts_kv_read(const itts_kv *kv, int32_t layer, int32_t which_v, float *out) {
+  if (!kv || !out) return set_error(ITTS_E_VALIDATION, "kv_cache: null argument");
+  const itts_config &c = kv->gpt->cfg;
+  if (layer < 0 || layer >= c.n_layer) return set_error(ITTS_E_VALIDATION, "layer: out of range");
+  HIP_TRY(hipStreamSynchronize(kv->gpt->stream));
+  const size_t es = kv->kvt == kKvBf16 ? 2 : 4;
+  std::vector<uint8_t> tmp((size_t)kv->valid_len * 64 * es);
+  for (int h = 0; h < c.n_head; h++) {
+    const char *src = static_cast<const char *>(which_v ? kv->v_layer(layer) : kv->k_layer(layer)) +
+                      (size_t)h * kv->max_seq * 64 * es;
+    if (kv->valid_len == 0) continue;
+    HIP_TRY(hipMemcpy(tmp.data(), src, tmp.size(), hipMemcpyDeviceToHost));
+    float *dst = out + (size_t)h * kv->valid_len * 64;
+    for (size_t i = 0; i < (size_t)kv->valid_len * 64; i++) {
+      if (es == 2) {
+        uint32_t b = (uint32_t)reinterpret_cast<const uint16_t *>(tmp.data())[i] << 16;
+        memcpy(&dst[i], &b, 4);
+      } else {
+        dst[i] = reinterpret_cast<const float *>(tmp.data())[i];
+      }
+    }
+  }
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_prefill_after(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens,
+                                   int32_t n_text, const float *conds, int32_t n_cond,
+                                   int32_t lang_id, const int32_t *prior_codes, int32_t n_prior,
+                                   float *logits_out) {
+  if (!gpt || !kv || kv->gpt != gpt) return set_error(ITTS_E_VALIDATION, "kv_cache: cache belongs to another decoder");
+  int T = 0;
+  itts_status st = run_prefill(gpt, kv, text_tokens, n_text, conds, n_cond, lang_id, prior_codes, n_prior, &T);
+  if (st) return st;
+  if (logits_out)
+    HIP_TRY(hipMemcpyAsync(logits_out, gpt->logits.p, sizeof(float) * gpt->cfg.mel_vocab,
+                           hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_prefill(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens, int32_t n_text,
+                             const float *conds, int32_t n_cond, int32_t lang_id, float *logits_out) {
+  return itts_gpt_prefill_after(gpt, kv, text_tokens, n_text, conds, n_cond, lang_id, nullptr, 0,
+                                logits_out);
+}
+
+itts_status itts_gpt_step(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int32_t pos_idx,
+                          float *logits_out) {
+  if (!gpt || !kv || kv->gpt != gpt) return set_error(ITTS_E_VALIDATION, "kv_cache: cache belongs to another decoder");
+  const itts_config &c = gpt->cfg;
+  if (mel_token_id < 0 || mel_token_id >= c.mel_vocab)
+    return set_error(ITTS_E_VALIDATION, "mel_token_id: mel_token_id %d out of range 0..%d", mel_token_id,
+                     c.mel_vocab);
+  if (pos_idx < 0 || pos_idx >= c.mel_pos_len)
+    return set_error(ITTS_E_VALIDATION, "pos_idx: pos_idx %d out of range 0..%d", pos_idx, c.mel_pos_len);
+  if (kv->valid_len + 1 > kv->max_seq)
+    return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
+                     kv->valid_len + 1, kv->max_seq);
+  DecodeCtl h{};
+  h.tok = mel_token_id;
+  h.pos = pos_idx;
+  h.valid_len = kv->valid_len;
+  if (itts_status st = write_ctl(kv, h)) return st;
+  if (itts_status st = enqueue_decode_step(gpt, kv)) return st;
+  if (logits_out)
+    HIP_TRY(hipMemcpyAsync(logits_out, gpt->logits.p, sizeof(float) * c.mel_vocab, hipMemcpyDeviceToHost,
+                           gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  kv->valid_len += 1;
+  return ITTS_OK;
+}
+
+uint64_t itts_rng_new(uint64_t seed) { return seed ^ 0x9E3779B97F4A7C15ull; }
+
+uint64_t itts_rng_next_u64(uint64_t *state) {
+  *state += 0x9E3779B97F4A7C15ull;
+  uint64_t z = *state;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+float itts_rng_next_f32(uint64_t *state) {
+  const uint32_t upper = (uint32_t)(itts_rng_next_u64(state) >> 40);
+  return (float)upper * (1.0f / 16777216.0f);
+}
+
+void itts_seen_init(uint64_t words[129]) {
+  memset(words, 0, 129 * sizeof(uint64_t));
+  itts_seen_insert(words, 1);
+  itts_seen_insert(words, 8192);
+}
+
+void itts_seen_insert(uint64_t words[129], int32_t token_id) {
+  if (token_id >= 0 && token_id < 129 * 64) words[token_id / 64] |= 1ull << (token_id % 64);
+}
+
+itts_status itts_sample_next_token(itts_gpt *gpt, float *logits, int32_t n, const uint64_t seen[129],
+                                   const itts_sampling *p, uint64_t *rng_state, int32_t *token_out) {
+  if (!gpt || !logits || !seen || !rng_state || !token_out)
+    return set_error(ITTS_E_VALIDATION, "logits: null argument");
+  if (n <= 0) return set_error(ITTS_E_VALIDATION, "logits: logits slice must not be empty");
+  if (n > 9216) return set_error(ITTS_E_VALIDATION, "logits: at most 9216 logits");
+  if (itts_status st = itts_sampling_validate(p)) return st;
+  hipStream_t s = gpt->stream;
+  HIP_TRY(gpt->s_logits.ensure(sizeof(float) * n));
+  HIP_TRY(gpt->s_seen.ensure(sizeof(uint64_t) * 129));
+  HIP_TRY(gpt->s_rng.ensure(sizeof(uint64_t)));
+  HIP_TRY(gpt->s_tok.ensure(sizeof(int32_t)));
+  HIP_TRY(hipMemcpyAsync(gpt->s_logits.p, logits, sizeof(float) * n, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(gpt->s_seen.p, seen, sizeof(uint64_t) * 129, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(gpt->s_rng.p, rng_state, sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  HIP_TRY(launch_sampler(gpt->s_logits.as<float>(), n, gpt->s_seen.as<uint64_t>(), to_dev_sampling(*p, n),
+                         gpt->s_rng.as<uint64_t>(), gpt->s_tok.as<int32_t>(), nullptr, nullptr, -1, 0, s));
+  HIP_TRY(hipMemcpyAsync(logits, gpt->s_logits.p, sizeof(float) * n, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(rng_state, gpt->s_rng.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(token_out, gpt->s_tok.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return ITTS_OK;
+}
+
+static bool same_sampling(const DevSampling &a, const DevSampling &b) {
+  return memcmp(&a, &b, sizeof(DevSampling)) == 0;
+}
+
+itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_code_prompt *prompt,
+                                      const itts_sampling *p, uint64_t *rng_state, int32_t *codes_out,
+                                      int32_t codes_cap, int32_t *n_codes) {
+  if (!gpt || !kv || !prompt || !rng_state || !codes_out || !n_codes)
+    return set_error(ITTS_E_VALIDATION, "generate: null argument");
+  if (kv->gpt != gpt) return set_error(ITTS_E_VALIDATION, "kv_cache: cache belongs to another decoder");
+  if (itts_status st = itts_sampling_validate(p)) return st;
+  const itts_config &c = gpt->cfg;
+  const int room = std::max(0, c.mel_pos_len - 3 - prompt->n_prior);
+  const int max_steps = std::min<int>((int)p->max_mel_tokens, room);
+  if (max_steps == 0)
+    return set_error(ITTS_E_VALIDATION,
+                     "max_mel_tokens: no Mel positions left to generate (max_mel_tokens is 0 or the prior "
+                     "codes fill the capacity)");
+  if (codes_cap < max_steps) return set_error(ITTS_E_VALIDATION, "codes_out: capacity %d < %d", codes_cap, max_steps);
+  if (prompt->min_codes < 0) return set_error(ITTS_E_VALIDATION, "min_codes: negative");
+  int T = 0;
+  itts_status st = run_prefill(gpt, kv, prompt->text_tokens, prompt->n_text, prompt->conds, prompt->n_cond,
+                               prompt->lang_id, prompt->prior_codes, prompt->n_prior, &T);
+  if (st) return st;
+  // Sample s is followed by a step that writes cache row T + s; the reference fails that
+  // step with a KV-capacity error once T + s + 1 > max_seq (gpt.rs:157-165).  The device
+  // loop therefore runs at most max_seq - T + 1 samples and reports the overflow if it
+  // gets there without STOP.
+  const int fit = kv->max_seq - T + 1;
+  const int dev_steps = std::min(max_steps, fit);
+  DecodeCtl h{};
+  h.valid_len = T;
+  h.min_codes = prompt->min_codes;
+  h.max_steps = dev_steps;
+  h.n_prior = prompt->n_prior;
+  h.rng = *rng_state;
+  h.last_tok = -1;
+  // prior codes are not added to the penalty set (sampler.rs:365-368)
+  memset(h.seen, 0, sizeof h.seen);
+  h.seen[0] |= 1ull << 1;
+  const int start_mel = c.mel_vocab - 2;
+  h.seen[start_mel / 64] |= 1ull << (start_mel % 64);
+  if ((st = write_ctl(kv, h))) return st;
+
+  const DevSampling ds = to_dev_sampling(*p, c.mel_vocab);
+  // capture one decode iteration (sample, then step) once per cache and parameters
+  if (!kv->have_graph || !same_sampling(kv->gkey, ds)) {
+    if (kv->gexec) {
+      (void)hipGraphExecDestroy(kv->gexec);
+      kv->gexec = nullptr;
+    }
+    if (kv->graph) {
+      (void)hipGraphDestroy(kv->graph);
+      kv->graph = nullptr;
+    }
+    kv->have_graph = false;
+    HIP_TRY(hipStreamSynchronize(gpt->stream));
+    HIP_TRY(hipStreamBeginCapture(gpt->stream, hipStreamCaptureModeThreadLocal));
+    hipError_t le = launch_sampler(gpt->logits.as<float>(), c.mel_vocab, nullptr, ds, nullptr, nullptr,
+                                   kv->ctl.as<DecodeCtl>(), kv->codes.as<int32_t>(), c.mel_vocab - 1, 1,
+                                   gpt->stream);
+    itts_status es = le == hipSuccess ? enqueue_decode_step(gpt, kv)
+                                      : set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
+    hipGraph_t graph = nullptr;
+    hipError_t ce = hipStreamEndCapture(gpt->stream, &graph);
+    if (es) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return es;
+    }
+    HIP_TRY(ce);
+    kv->graph = graph;
+    HIP_TRY(hipGraphInstantiate(&kv->gexec, kv->graph, nullptr, nullptr, 0));
+    kv->gkey = ds;
+    kv->have_graph = true;
+  }
+  // Replay in batches, keeping one batch in flight while the previous one's control
+  // block is inspected; iterations after `done` exit at their first instruction.
+  const int batch = 8;
+  DecodeCtl *slot[2] = {kv->host_ctl, kv->host_ctl + 1};
+  hipEvent_t ev[2];
+  HIP_TRY(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+  if (hipEventCreateWithFlags(&ev[1], hipEventDisableTiming) != hipSuccess) {
+    (void)hipEventDestroy(ev[0]);
+    return set_error(ITTS_E_DEVICE, "hipEventCreate failed");
+  }
+  auto cleanup = [&]() {
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+  };
+  auto launch_batch = [&](int which) -> hipError_t {
+    for (int i = 0; i < batch; i++) {
+      hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
+      if (e != hipSuccess) return e;
+    }
+    hipError_t e = hipMemcpyAsync(slot[which], kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost,
+                                  gpt->stream);
+    if (e != hipSuccess) return e;
+    return hipEventRecord(ev[which], gpt->stream);
+  };
+  // Each iteration samples once and `done` is set by step max_steps-1 at the latest, so
+  // ceil(max_steps / batch) batches always reach the end.
+  const int nb_total = (max_steps + batch - 1) / batch;
+  int nb = 0;
+  hipError_t e = launch_batch(0);
+  nb = 1;
+  for (int i = 0; e == hipSuccess; i++) {
+    if (nb < nb_total) {
+      e = launch_batch(nb & 1);
+      nb++;
+      if (e != hipSuccess) break;
+    }
+    e = hipEventSynchronize(ev[i & 1]);
+    if (e != hipSuccess) break;
+    if (slot[i & 1]->done || i + 1 >= nb_total) break;
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(gpt->stream);
+  cleanup();
+  HIP_TRY(e);
+  DecodeCtl fin{};
+  HIP_TRY(hipMemcpy(&fin, kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost));
+  if (!fin.done) return set_error(ITTS_E_INTERNAL, "generation did not reach its end");
+  kv->valid_len = fin.valid_len;
+  if (dev_steps < max_steps && fin.n_codes == dev_steps)
+    return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
+                     kv->max_seq + 1, kv->max_seq);
+  HIP_TRY(hipMemcpy(codes_out, kv->codes.p, sizeof(int32_t) * fin.n_codes, hipMemcpyDeviceToHost));
+  *n_codes = fin.n_codes;
+  *rng_state = fin.rng;
+  kv->valid_len = fin.valid_len;
+  return ITTS_OK;
+}
+
+itts_status itts_generate_codes(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens, int32_t n_text,
+                                const float *conds, int32_t n_cond, int32_t lang_id, const itts_sampling *p,
+                                uint64_t *rng_state, int32_t *codes_out, int32_t codes_cap, int32_t *n_codes) {
+  itts_code_prompt pr{};
+  pr.text_tokens = text_tokens;
+  pr.n_text = n_text;
+  pr.conds = conds;
+  pr.n_cond = n_cond;
+  pr.lang_id = lang_id;
+  return itts_generate_codes_after(gpt, kv, &pr, p, rng_state, codes_out, codes_cap, n_codes);
+}
+
+// ---- quantiser ----
+
+static inline uint16_t f32_to_f16_rne(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (ax < 0x38800000u) {
+    if (ax < 0x33000000u) return (uint16_t)sign;
+    const uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u, sh = 126 - e;
+    uint32_t h = m >> sh;
+    const uint32_t rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = (ax >> 13) - (112u << 10);
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+static inline float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  float out;
+  if (e == 0) {
+    out = (float)m * 5.9604644775390625e-08f;
+    return sign ? -out : out;
+  }
+  const uint32_t bits = e == 31 ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+  memcpy(&out, &bits, 4);
+  return out;
+}
+
+itts_status itts_quantize(const float *w, int32_t N, int32_t K, int32_t bits, itts_dtype param_dtype,
+                          void *codes, void *scales, void *biases) {
+  if (!w || !codes || !scales || !biases) return set_error(ITTS_E_VALIDATION, "quantize: null argument");
+  if (N <= 0 || K <= 0 || K % 64 != 0) return set_error(ITTS_E_VALIDATION, "quantize: K must be a multiple of 64");
+  if (bits != 8 && bits != 4) return set_error(ITTS_E_VALIDATION, "quantize: bits must be 8 or 4");
+  if (param_dtype != ITTS_F16 && param_dtype != ITTS_F32)
+    return set_error(ITTS_E_VALIDATION, "quantize: param_dtype must be F16 or F32");
+  const int G = K / 64;
+  const float levels = bits == 8 ? 255.0f : 15.0f;
+  const bool f32 = param_dtype == ITTS_F32;
+  uint8_t *cb = static_cast<uint8_t *>(codes);
+  auto work = [&](int r0, int r1) {
+    for (int o = r0; o < r1; o++) {
+      if (bits == 4) memset(cb + (size_t)o * (K / 2), 0, K / 2);
+      for (int g = 0; g < G; g++) {
+        const float *p = w + (size_t)o * K + (size_t)g * 64;
+        float mn = p[0], mx = p[0];
+        for (int i = 1; i < 64; i++) {
+          mn = p[i] < mn ? p[i] : mn;
+          mx = p[i] > mx ? p[i] : mx;
+        }
+        float s = (mx - mn) / levels, b = mn;
+        const size_t gi = (size_t)o * G + g;
+        if (f32) {
+          static_cast<float *>(scales)[gi] = s;
+          static_cast<float *>(biases)[gi] = b;
+        } else {
+          const uint16_t sh = f32_to_f16_rne(s), bh = f32_to_f16_rne(b);
+          static_cast<uint16_t *>(scales)[gi] = sh;
+          static_cast<uint16_t *>(biases)[gi] = bh;
+          s = f16_to_f32(sh);
+          b = f16_to_f32(bh);
+        }
+        for (int i = 0; i < 64; i++) {
+          float q = 0.0f;
+          if (s != 0.0f) {
+            q = std::rint((p[i] - b) / s);
+            q = q < 0.0f ? 0.0f : (q > levels ? levels : q);
+          }
+          const int k = g * 64 + i;
+          if (bits == 8) cb[(size_t)o * K + k] = (uint8_t)q;
+          else cb[(size_t)o * (K / 2) + k / 2] |= (uint8_t)((int)q << ((k & 1) * 4));
+        }
+      }
+    }
+  };
+  const int nt = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> th;
+  const int per = (N + nt - 1) / nt;
+  for (int t = 0; t < nt; t++) {
+    const int r0 = t * per, r1 = std::min(N, r0 + per);
+    if (r0 < r1) th.emplace_back(work, r0, r1);
+  }
+  for (auto &t : th) t.join();
+  return ITTS_OK;
+}
+
+// ---- kernel-level entry points ----
+
+static itts_status temp_ql(QLHost &q, const itts_qlinear *ql, int N, int K, int bits, itts_dtype pd) {
+  if (!ql) return set_error(ITTS_E_VALIDATION, "qlinear: null");
+  if (N <= 0 || K <= 0 || K % 64) return set_error(ITTS_E_VALIDATION, "qlinear: K must be a multiple of 64");
+  if (bits != 8 && bits != 4) return set_error(ITTS_E_VALIDATION, "qlinear: bits must be 8 or 4");
+  if (pd != ITTS_F16 && pd != ITTS_F32) return set_error(ITTS_E_VALIDATION, "qlinear: param dtype");
+  std::vector<float> zero;
+  itts_qlinear tmp = *ql;
+  if (!tmp.bias) {
+    zero.assign(N, 0.0f);
+    tmp.bias = zero.data();
+  }
+  return upload_ql(q, tmp, N, K, bits, pd == ITTS_F32, "qlinear");
+}
+
+itts_status itts_dequantize(itts_gpt *gpt, const itts_qlinear *ql, int32_t N, int32_t K, int32_t bits,
+                            itts_dtype param_dtype, float *out) {
+  if (!gpt || !out) return set_error(ITTS_E_VALIDATION, "dequantize: null argument");
+  QLHost q;
+  if (itts_status st = temp_ql(q, ql, N, K, bits, param_dtype)) return st;
+  DevBuf o;
+  HIP_TRY(o.ensure(sizeof(float) * (size_t)N * K));
+  HIP_TRY(launch_dequant(q.dev(), bits, param_dtype == ITTS_F32 ? kParamF32 : kParamF16, o.as<float>(),
+                         gpt->stream));
+  HIP_TRY(hipMemcpyAsync(out, o.p, sizeof(float) * (size_t)N * K, hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  return ITTS_OK;
+}
+
+itts_status itts_qlinear_forward(itts_gpt *gpt, const itts_qlinear *ql, int32_t N, int32_t K, int32_t bits,
+                                 itts_dtype param_dtype, const float *x, int32_t M, float *y) {
+  if (!gpt || !x || !y || M <= 0) return set_error(ITTS_E_VALIDATION, "qlinear: bad argument");
+  QLHost q;
+  if (itts_status st = temp_ql(q, ql, N, K, bits, param_dtype)) return st;
+  const int epc = bits == 8 ? 16 : 32;
+  if (M == 1 && K / epc > 512) return set_error(ITTS_E_VALIDATION, "qlinear: K too large for the GEMV");
+  DevBuf dx, dy;
+  HIP_TRY(dx.ensure(sizeof(float) * (size_t)M * K));
+  HIP_TRY(dy.ensure(sizeof(float) * (size_t)M * N));
+  HIP_TRY(hipMemcpyAsync(dx.p, x, sizeof(float) * (size_t)M * K, hipMemcpyHostToDevice, gpt->stream));
+  const int pt = param_dtype == ITTS_F32 ? kParamF32 : kParamF16;
+  if (M == 1) {
+    GemvArgs a{};
+    a.ql = q.dev();
+    a.x = dx.as<float>();
+    a.y = dy.as<float>();
+    HIP_TRY(launch_gemv(a, bits, pt, kProNone, kEpiStore, kKvBf16, gpt->stream));
+  } else {
+    GemmArgs a{};
+    a.ql = q.dev();
+    a.x = dx.as<float>();
+    a.M = M;
+    a.y = dy.as<float>();
+    HIP_TRY(launch_gemm(a, bits, pt, kEpiStore, kKvBf16, gpt->stream));
+  }
+  HIP_TRY(hipMemcpyAsync(y, dy.p, sizeof(float) * (size_t)M * N, hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  return ITTS_OK;
+}
+
+}  // extern "C"

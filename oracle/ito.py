@@ -1,0 +1,286 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libitts_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, never by the product package.  See itts_oracle.h for what each
+function restates and the reference lines it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libitts_oracle.so")
+
+ITO_OK, ITO_E_VALIDATION, ITO_E_CAPACITY, ITO_E_ALLOC = 0, 1, 4, 5
+ITO_F32, ITO_F64 = 0, 1
+ITO_KV_F32, ITO_KV_BF16 = 0, 1
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+        self.message = message
+
+
+class ito_config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_layer", "d_model", "n_head", "d_ffn", "mel_vocab", "text_vocab", "lang_vocab",
+        "mel_pos_len", "text_pos_len", "bits", "param_f32")]
+
+
+class ito_ql(C.Structure):
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("bias", C.c_void_p), ("N", C.c_int32), ("K", C.c_int32)]
+
+
+class ito_layer(C.Structure):
+    _fields_ = [("ln1_w", C.c_void_p), ("ln1_b", C.c_void_p), ("c_attn", ito_ql),
+                ("c_proj", ito_ql), ("ln2_w", C.c_void_p), ("ln2_b", C.c_void_p),
+                ("c_fc", ito_ql), ("mlp_proj", ito_ql)]
+
+
+class ito_model(C.Structure):
+    _fields_ = [("cfg", ito_config), ("text_emb", C.c_void_p), ("lang_emb", C.c_void_p),
+                ("mel_emb", C.c_void_p), ("mel_pos", C.c_void_p), ("text_pos", C.c_void_p),
+                ("layers", C.POINTER(ito_layer)), ("ln_f_w", C.c_void_p), ("ln_f_b", C.c_void_p),
+                ("fn_w", C.c_void_p), ("fn_b", C.c_void_p), ("head", ito_ql)]
+
+
+class ito_sampling(C.Structure):
+    _fields_ = [("greedy", C.c_int32), ("temperature", C.c_float), ("top_p", C.c_float),
+                ("top_k", C.c_uint32), ("repetition_penalty", C.c_float),
+                ("max_mel_tokens", C.c_uint32)]
+
+
+P = C.c_void_p
+_SIGS = {
+    "ito_half_to_float": (C.c_float, [C.c_uint16]),
+    "ito_float_to_half": (C.c_uint16, [C.c_float]),
+    "ito_float_to_bf16": (C.c_uint16, [C.c_float]),
+    "ito_bf16_to_float": (C.c_float, [C.c_uint16]),
+    "ito_expf": (C.c_float, [C.c_float]),
+    "ito_rng_init": (C.c_uint64, [C.c_uint64]),
+    "ito_rng_next_u64": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+    "ito_rng_next_f32": (C.c_float, [C.POINTER(C.c_uint64)]),
+    "ito_quantize": (C.c_int, [P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, P, P, P]),
+    "ito_dequant": (C.c_int, [C.POINTER(ito_ql), C.c_int32, C.c_int32, P]),
+    "ito_ql_forward": (C.c_int, [C.POINTER(ito_ql), C.c_int32, C.c_int32, C.c_int32, P, C.c_int32, P]),
+    "ito_layernorm": (None, [P, P, P, C.c_int32, C.c_float, P]),
+    "ito_gelu": (C.c_float, [C.c_float]),
+    "ito_kv_create": (C.c_int, [C.POINTER(ito_config), C.c_int32, C.c_int32, C.c_int32,
+                                C.POINTER(C.c_void_p)]),
+    "ito_kv_destroy": (None, [P]),
+    "ito_kv_reset": (None, [P]),
+    "ito_kv_valid_len": (C.c_int32, [P]),
+    "ito_kv_read": (C.c_int, [P, C.c_int32, C.c_int32, P]),
+    "ito_prefill_after": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32, P,
+                                    C.c_int32, C.c_int32, P, C.c_int32, P]),
+    "ito_step": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, C.c_int32, C.c_int32, P]),
+    "ito_forward_rows": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32, C.c_int32, P]),
+    "ito_sequence_embedding": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32,
+                                         C.c_int32, P, C.c_int32, P]),
+    "ito_sampling_validate": (C.c_int, [C.POINTER(ito_sampling)]),
+    "ito_seen_init": (None, [P, C.c_int32]),
+    "ito_seen_insert": (None, [P, C.c_int32]),
+    "ito_apply_repetition_penalty": (None, [P, P, C.c_int32, C.c_float]),
+    "ito_argmax_finite": (C.c_int32, [P, C.c_int32]),
+    "ito_sample_next_token": (C.c_int, [P, C.c_int32, P, C.POINTER(ito_sampling),
+                                        C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
+    "ito_generate_codes_after": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32, P,
+                                           C.c_int32, C.c_int32, P, C.c_int32, C.c_int32,
+                                           C.POINTER(ito_sampling), C.POINTER(C.c_uint64), P,
+                                           C.c_int32, C.POINTER(C.c_int32), P]),
+    "ito_last_error": (C.c_char_p, []),
+    "ito_set_threads": (None, [C.c_int32]),
+}
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def check(st):
+    if st != ITO_OK:
+        raise OracleError(st, lib.ito_last_error().decode(errors="replace"))
+
+
+def _ql(q) -> ito_ql:
+    return ito_ql(q.codes.ctypes.data, q.scales.ctypes.data, q.biases.ctypes.data,
+                  q.bias.ctypes.data, q.N, q.K)
+
+
+class Model:
+    """An ito_model view over itts_hip.synth.ModelWeights (same host arrays)."""
+
+    def __init__(self, w):
+        self.w = w
+        c = w.cfg
+        self.cfg = ito_config(c["n_layer"], c["d_model"], c["n_head"], c["d_ffn"], c["mel_vocab"],
+                              c["text_vocab"], c["lang_vocab"], c["mel_pos_len"], c["text_pos_len"],
+                              c["quant_bits"], 1 if c["param_dtype"] == 2 else 0)
+        self.layers = (ito_layer * len(w.layers))()
+        for i, L in enumerate(w.layers):
+            self.layers[i] = ito_layer(L.ln1_w.ctypes.data, L.ln1_b.ctypes.data, _ql(L.c_attn),
+                                       _ql(L.c_proj), L.ln2_w.ctypes.data, L.ln2_b.ctypes.data,
+                                       _ql(L.c_fc), _ql(L.mlp_c_proj))
+        self.m = ito_model(self.cfg, w.text_emb.ctypes.data, w.lang_emb.ctypes.data,
+                           w.mel_emb.ctypes.data, w.mel_pos.ctypes.data, w.text_pos.ctypes.data,
+                           C.cast(self.layers, C.POINTER(ito_layer)), w.ln_f_w.ctypes.data,
+                           w.ln_f_b.ctypes.data, w.fn_w.ctypes.data, w.fn_b.ctypes.data,
+                           _ql(w.head))
+
+    @property
+    def ref(self):
+        return C.byref(self.m)
+
+    def kv(self, max_seq=2048, kv_bf16=True, mode=ITO_F32) -> "KV":
+        return KV(self, max_seq, kv_bf16, mode)
+
+    def prefill_after(self, kv, text, conds, lang_id, prior=()):
+        t = np.ascontiguousarray(text, np.int32)
+        c = np.ascontiguousarray(conds, np.float32).reshape(-1, self.w.cfg["d_model"])
+        pr = np.ascontiguousarray(prior, np.int32)
+        out = np.empty(self.w.cfg["mel_vocab"], np.float32)
+        check(lib.ito_prefill_after(self.ref, kv.h, kv.mode, _p(t), len(t), _p(c), c.shape[0],
+                                    int(lang_id), _p(pr), len(pr), _p(out)))
+        return out
+
+    def step(self, kv, tok, pos):
+        out = np.empty(self.w.cfg["mel_vocab"], np.float32)
+        check(lib.ito_step(self.ref, kv.h, kv.mode, int(tok), int(pos), _p(out)))
+        return out
+
+    def sequence_embedding(self, text, conds, lang_id, prior=()):
+        t = np.ascontiguousarray(text, np.int32)
+        c = np.ascontiguousarray(conds, np.float32).reshape(-1, self.w.cfg["d_model"])
+        pr = np.ascontiguousarray(prior, np.int32)
+        T = c.shape[0] + len(t) + 3 + len(pr)
+        out = np.empty((T, self.w.cfg["d_model"]), np.float32)
+        check(lib.ito_sequence_embedding(self.ref, _p(t), len(t), _p(c), c.shape[0], int(lang_id),
+                                         _p(pr), len(pr), _p(out)))
+        return out
+
+    def forward_rows(self, kv, emb, row0=0):
+        emb = np.ascontiguousarray(emb, np.float32)
+        T = emb.shape[0]
+        out = np.empty((T - row0, self.w.cfg["mel_vocab"]), np.float32)
+        check(lib.ito_forward_rows(self.ref, kv.h, kv.mode, _p(emb), T, row0, _p(out)))
+        return out
+
+    def generate_codes_after(self, kv, text, conds, lang_id, params, rng_state, prior=(),
+                             min_codes=0):
+        t = np.ascontiguousarray(text, np.int32)
+        c = np.ascontiguousarray(conds, np.float32).reshape(-1, self.w.cfg["d_model"])
+        pr = np.ascontiguousarray(prior, np.int32)
+        sp = sampling(params)
+        cap = max(1, int(params.max_mel_tokens))
+        out = np.empty(cap, np.int32)
+        first = np.empty(self.w.cfg["mel_vocab"], np.float32)
+        n = C.c_int32()
+        st = C.c_uint64(rng_state)
+        check(lib.ito_generate_codes_after(self.ref, kv.h, kv.mode, _p(t), len(t), _p(c), c.shape[0],
+                                           int(lang_id), _p(pr), len(pr), int(min_codes),
+                                           C.byref(sp), C.byref(st), _p(out), cap, C.byref(n),
+                                           _p(first)))
+        return out[: n.value].copy(), st.value, first
+
+
+class KV:
+    def __init__(self, model, max_seq, kv_bf16, mode):
+        self.model = model
+        self.mode = mode
+        h = C.c_void_p()
+        check(lib.ito_kv_create(C.byref(model.cfg), int(max_seq), ITO_KV_BF16 if kv_bf16 else ITO_KV_F32,
+                                mode, C.byref(h)))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.ito_kv_destroy(self.h)
+            self.h = None
+
+    def valid_len(self):
+        return lib.ito_kv_valid_len(self.h)
+
+    def reset(self):
+        lib.ito_kv_reset(self.h)
+
+    def read(self, layer, which_v):
+        c = self.model.w.cfg
+        out = np.empty((c["n_head"], self.valid_len(), 64), np.float32)
+        check(lib.ito_kv_read(self.h, layer, int(which_v), _p(out)))
+        return out
+
+
+def sampling(params) -> ito_sampling:
+    return ito_sampling(int(bool(params.greedy)), float(params.temperature), float(params.top_p),
+                        int(params.top_k), float(params.repetition_penalty), int(params.max_mel_tokens))
+
+
+def quantize(w, bits=8, param_dtype=1):
+    """Oracle quantiser with the itts_hip.quantize calling convention (1 = fp16, 2 = fp32)."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    codes = np.empty((N, K * bits // 8), np.uint8)
+    f32 = param_dtype == 2
+    pdt = np.float32 if f32 else np.uint16
+    scales = np.empty((N, K // 64), pdt)
+    biases = np.empty((N, K // 64), pdt)
+    check(lib.ito_quantize(_p(w), N, K, bits, int(f32), _p(codes), _p(scales), _p(biases)))
+    return codes, scales, biases
+
+
+def dequant(q, bits, param_dtype):
+    out = np.empty((q.N, q.K), np.float32)
+    ql = _ql(q)
+    check(lib.ito_dequant(C.byref(ql), bits, 1 if param_dtype == 2 else 0, _p(out)))
+    return out
+
+
+def ql_forward(q, bits, param_dtype, x, mode=ITO_F32):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, q.K)
+    out = np.empty((x.shape[0], q.N), np.float32)
+    ql = _ql(q)
+    check(lib.ito_ql_forward(C.byref(ql), bits, 1 if param_dtype == 2 else 0, mode, _p(x), x.shape[0],
+                             _p(out)))
+    return out
+
+
+def sample_next_token(logits, seen_words, params, rng_state):
+    """Returns (token, new rng state); logits are penalised in place."""
+    assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+    sp = sampling(params)
+    st = C.c_uint64(rng_state)
+    tok = C.c_int32()
+    check(lib.ito_sample_next_token(_p(logits), len(logits), _p(seen_words), C.byref(sp), C.byref(st),
+                                    C.byref(tok)))
+    return tok.value, st.value
+
+
+def seen_init(start_mel=8192):
+    w = np.zeros(129, np.uint64)
+    lib.ito_seen_init(_p(w), start_mel)
+    return w
