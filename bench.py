@@ -1,0 +1,214 @@
+"""Benchmark of the int8 GPT-2 semantic-token decoder on one MI355X.
+
+Workload (default): the long-utterance configuration — 24 layers, d_model 1280,
+20 heads, int8 group-64 weights with fp16 group params (seeded N(0, 0.02) init),
+batch 1, prefill 32 conditioning rows + 200 text tokens (235 rows), then 1500 sampled
+decode steps (temperature 0.8, top-k 30, top-p 0.8, repetition penalty 10, fixed seed,
+STOP masked so the length is fixed), bf16 KV cache growing to 1734 rows.
+
+One benchmark step = one whole generation (prefill + 1500 sampled tokens) through
+itts_generate_codes_after, inputs already resident on the device.  `value` is generated
+tokens per second over the timed steps (prefill included).  The decode step (one
+replay of the captured sample+step graph) is the unit whose HBM roofline is reported:
+achieved = algorithmic bytes of one decode step / its average device time (HIP events
+on the decoder's stream).
+
+Usage: python bench.py [--steps K] [--warmup W] [--workload long|short|int4]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "index-tts-rs_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "batch-1 decode tokens/s (int8, 24L d1280); % of HBM roofline; TTFT"
+HBM_PEAK_GBS = 8000.0
+KV_ROW_BYTES = 24 * 2 * 20 * 64 * 2  # one position of K and V over 24 layers, bf16
+
+WORKLOADS = {
+    # name: (n_cond, n_text, steps, sampling, bits, description)
+    "long": (32, 200, 1500, dict(greedy=False, temperature=0.8, top_k=30, top_p=0.8,
+                                  repetition_penalty=10.0),
+             8, "batch 1, prefill 32 cond + 200 text (235 rows), 1500 sampled steps "
+                "(T 0.8, top-k 30, top-p 0.8, penalty 10), bf16 KV to 1734 rows"),
+    "short": (32, 64, 128, dict(greedy=True, repetition_penalty=10.0), 8,
+              "batch 1, prefill 32 cond + 64 text (99 rows), 128 greedy steps"),
+    "int4": (32, 128, 1500, dict(greedy=True, repetition_penalty=10.0), 4,
+             "int4 weights, batch 1, prefill 32 + 128 text (163 rows), 1500 greedy steps"),
+}
+
+
+def hip():
+    lib = C.CDLL("libamdhip64.so")
+    lib.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    lib.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+    lib.hipEventSynchronize.argtypes = [C.c_void_p]
+    lib.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    lib.hipDeviceSynchronize.argtypes = []
+    return lib
+
+
+def step_bytes(weight_bytes: int, L: int) -> int:
+    """Algorithmic HBM bytes of one decode step with L keys (the new row included):
+    every weight byte once, the K/V rows 0..L-1 once, the new K/V row written, the
+    logits written."""
+    return weight_bytes + KV_ROW_BYTES * L + KV_ROW_BYTES + 8194 * 4
+
+
+def cpu_baseline(W, prompt, sp, n_steps: int):
+    """The oracle (CPU restatement of the reference decoder) on the same weights and
+    prompt: prefill, then n_steps sampled decode steps; threads = host cores (<= 16)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ito
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    ito.lib.ito_set_threads(threads)
+    M = ito.Model(W)
+    kv = M.kv(2048, kv_bf16=True)
+    t0 = time.perf_counter()
+    logits = M.prefill_after(kv, prompt.text_tokens, prompt.conds, prompt.lang_id)
+    t_prefill = time.perf_counter() - t0
+    seen = ito.seen_init()
+    state = ito.lib.ito_rng_init(1234)
+    t0 = time.perf_counter()
+    for s in range(n_steps):
+        logits[8193] = -np.inf
+        tok, state = ito.sample_next_token(logits, seen, sp, state)
+        ito.lib.ito_seen_insert(ito._p(seen), tok)
+        logits = M.step(kv, tok, s + 2)
+    t_dec = time.perf_counter() - t0
+    return {
+        "value": round(n_steps / t_dec, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle (C restatement of gpt.rs/sampler.rs, fp32, bf16 KV) on the same "
+                  f"weights: prefill {kv.valid_len() - n_steps} rows then {n_steps} sampled "
+                  f"decode steps; prefill took {t_prefill * 1e3:.0f} ms (CPU time to first "
+                  f"token), decode {t_dec * 1e3 / n_steps:.1f} ms/token",
+        "ttft_ms": round(t_prefill * 1e3, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="long", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the decoder runs one sequence per GPU and this "
+              "build has no multi-GPU path (requests shard by sequence). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import itts_hip as H
+    from itts_hip import synth
+
+    n_cond, n_text, n_steps, samp, bits, desc = WORKLOADS[args.workload]
+    cfg = dict(synth.FULL_CONFIG, quant_bits=bits)
+    t0 = time.perf_counter()
+    W = synth.make_weights(cfg, seed=args.seed)
+    weight_bytes = W.weight_bytes_per_step()
+    print(f"[bench] weights generated in {time.perf_counter() - t0:.1f}s "
+          f"({weight_bytes / 1e6:.1f} MB per decode step)", file=sys.stderr, flush=True)
+    g = H.Gpt(W)
+    kv = g.kv_cache(2048, H.ITTS_BF16)
+    prompt = synth.make_prompt(cfg, n_cond, n_text, seed=args.seed + 1)
+    sp = H.SamplingParams(max_mel_tokens=n_steps, **samp)
+    cp = H.CodePrompt(prompt.text_tokens, prompt.conds, prompt.lang_id, None, n_steps)
+    hp = hip()
+
+    def generate():
+        rng = H.SamplerRng(1234)
+        return H.generate_codes_after(g, cp, kv, sp, rng)
+
+    for _ in range(args.warmup):
+        codes = generate()
+        print(f"[bench] warmup generation: {len(codes)} codes", file=sys.stderr, flush=True)
+
+    # time to first token: host call -> first token id on the host (prefill + one sample)
+    sp1 = H.SamplingParams(max_mel_tokens=1, **samp)
+    ttft = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        H.generate_codes_after(g, H.CodePrompt(prompt.text_tokens, prompt.conds, prompt.lang_id, None, 1),
+                               kv, sp1, H.SamplerRng(1234))
+        ttft.append((time.perf_counter() - t0) * 1e3)
+    ttft_ms = statistics.median(ttft)
+
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    hp.hipEventCreate(C.byref(ev0))
+    hp.hipEventCreate(C.byref(ev1))
+    stream = C.c_void_p(g.stream)
+    hp.hipDeviceSynchronize()
+    timings = []
+    t0 = time.perf_counter()
+    hp.hipEventRecord(ev0, stream)
+    for _ in range(args.steps):
+        codes = generate()
+        timings.append(kv.last_timing())
+    hp.hipEventRecord(ev1, stream)
+    hp.hipEventSynchronize(ev1)
+    hp.hipDeviceSynchronize()
+    wall = time.perf_counter() - t0
+    region_ms = C.c_float()
+    hp.hipEventElapsedTime(C.byref(region_ms), ev0, ev1)
+    n_tok = len(codes)
+    assert n_tok == n_steps, (n_tok, n_steps)
+
+    T = timings[-1]["prefill_rows"]
+    dec_steps = timings[-1]["decode_steps"]
+    dec_ms = statistics.mean(t["decode_ms"] for t in timings)
+    pre_ms = statistics.mean(t["prefill_ms"] for t in timings)
+    step_ms = dec_ms / dec_steps
+    mean_L = T + (dec_steps + 1) / 2.0  # keys of step i: T + i + 1, i = 0..dec_steps-1
+    bytes_step = step_bytes(weight_bytes, int(round(mean_L)))
+    achieved = bytes_step / (step_ms * 1e-3) / 1e9
+    value = args.steps * n_tok / wall
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded random-init weights of the reference architecture)",
+        "config": {"workload": desc, "weights": f"int{bits} MLX-affine group 64, fp16 params",
+                   "kv_cache": "bf16", "layers": 24, "d_model": 1280, "heads": 20,
+                   "prefill_rows": T, "decode_tokens": n_tok, "step": "one full generation"},
+        "ttft_ms": round(ttft_ms, 3),
+        "decode_tokens_per_s": round(dec_steps / (dec_ms * 1e-3), 2),
+        "decode_step_us": round(step_ms * 1e3, 2),
+        "prefill_ms": round(pre_ms, 3),
+        "gpu_region_ms": round(region_ms.value, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "decode step (one replay of the sample+step graph)",
+                     "bytes_per_launch": bytes_step, "mean_keys": mean_L},
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(W, prompt, sp, args.cpu_steps)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -133,6 +133,8 @@ itts_status itts_sampling_validate(const itts_sampling *p);
 /* ---- Gpt (gpt.rs:438-525) ---- */
 /* Gpt::from_weights: validates the shape, uploads and repacks every tensor. */
 itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out);
+/* Releases the caller's handle.  Live KV caches keep the decoder's device state until
+ * they are destroyed too, so the two may be destroyed in either order. */
 void itts_gpt_destroy(itts_gpt *gpt);
 int32_t itts_gpt_num_layers(const itts_gpt *gpt);        /* Gpt::num_layers */
 int32_t itts_gpt_max_cond(const itts_gpt *gpt);
@@ -184,6 +186,18 @@ itts_status itts_sample_next_token(itts_gpt *gpt, float *logits, int32_t n,
 itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_code_prompt *prompt,
                                       const itts_sampling *p, uint64_t *rng_state,
                                       int32_t *codes_out, int32_t codes_cap, int32_t *n_codes);
+/* Device-side timing of the last generate call on this cache, from HIP events recorded
+ * on the decoder's stream (the counterpart of the reference's StageTimings.gpt_ms,
+ * crates/core/src/engine/stream.rs:19-44, split into its two phases). */
+typedef struct itts_timing {
+  float prefill_ms;      /* embedding + stack + head of the prompt rows */
+  float decode_ms;       /* sampling + decode steps until the end of the loop */
+  int32_t prefill_rows;  /* rows of the prompt */
+  int32_t decode_steps;  /* decode steps executed (KV rows appended) */
+  int32_t samples;       /* tokens sampled (STOP included) */
+} itts_timing;
+itts_status itts_kv_last_timing(const itts_kv *kv, itts_timing *out);
+
 /* generate_codes (sampler.rs:309-326): no prior codes, min_codes 0. */
 itts_status itts_generate_codes(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens,
                                 int32_t n_text, const float *conds, int32_t n_cond,

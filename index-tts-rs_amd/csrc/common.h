@@ -72,6 +72,25 @@ __device__ inline float half_bits_to_float(uint32_t h) {
 
 __device__ inline float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
 
+// IEEE operations that round on their own: never fused into an FMA with a neighbour
+// (hipcc contracts a*b+c by default, including through the __f*_rn helpers).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
+
 // Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
 __device__ inline uint32_t float_to_bf16_bits(float f) {
   uint32_t x = __float_as_uint(f);

@@ -8,7 +8,18 @@
 
 namespace itts {
 
-enum Prologue : int { kProNone = 0, kProLN = 1, kProLNLN = 2 };
+// kProEmbedLN: the input row is the step embedding mel_emb[ctl->tok] + mel_pos[ctl->pos]
+// (block 0 stores it to x_out as the residual stream), then LayerNorm.
+// kProAttn: the input row is the attention output, combined from the split partials of
+// the decode attention (attn.part / attn.n_head / attn.max_splits, L from ctl).
+enum Prologue : int { kProNone = 0, kProLN = 1, kProLNLN = 2, kProEmbedLN = 3, kProAttn = 4 };
+
+struct AttnPartials {
+  const float *part;  // [n_head][max_splits][66]: max, denominator, 64 outputs
+  int n_head;
+  int max_splits;
+  int static_len;     // key count when ctl == nullptr
+};
 enum Epilogue : int { kEpiStore = 0, kEpiResid = 1, kEpiGelu = 2, kEpiQKV = 3 };
 
 // Where the QKV epilogue scatters: q -> q_out[M][d]; k, v -> this layer's cache
@@ -30,24 +41,27 @@ struct GemvArgs {
   float *y;                // output row [N] (store / gelu) or residual stream (resid)
   QkvDst qkv;
   const DecodeCtl *ctl;    // optional: early exit when done, cache row = valid_len
+  const float *emb_tok, *emb_pos;  // kProEmbedLN tables (mel_emb, mel_pos)
+  float *x_out;            // kProEmbedLN: residual stream written by block 0
+  DecodeCtl *finish;       // optional: block 0 advances finish->valid_len after its rows
+  AttnPartials attn;       // kProAttn
 };
 
 hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi, int kvt,
                        hipStream_t s);
 
-// Decode attention: q [n_head*64] against cache rows 0..valid_len (inclusive of the
-// row the step just wrote), split over the keys; then the split combine.
+// Decode attention: q [n_head*64] against cache rows 0..L-1 with L = ctl->valid_len + 1
+// (or static_len), 256 keys per split.  Each split writes its partial (max, denominator,
+// 64 unnormalised outputs) to part [n_head][max_splits][66]; the consumer (the c_proj
+// GEMV's kProAttn prologue) combines them.
+int attn_decode_max_splits(int max_seq);
 hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, int n_head,
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,
-                              int max_splits, int chunk, float *out, int kvt, hipStream_t s);
+                              int kvt, hipStream_t s);
 
 // Causal attention of T rows at cache positions base..base+T-1 (prefill).
 hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
                                int n_head, int max_seq, float *out, int kvt, hipStream_t s);
-
-// x = mel_emb[ctl->tok] + mel_pos[ctl->pos]  (or the given tok/pos when ctl == nullptr)
-hipError_t launch_embed_step(const float *mel_emb, const float *mel_pos, const DecodeCtl *ctl,
-                             int d, float *x, hipStream_t s);
 
 // Row descriptors for the prefill embedding.
 struct EmbedRow {
@@ -85,8 +99,5 @@ hipError_t sampler_init();
 hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSampling p,
                           uint64_t *rng, int32_t *tok_out, DecodeCtl *ctl, int32_t *codes,
                           int stop_tok, int mode, hipStream_t s);
-
-// ctl->valid_len += 1 after a decode step (skipped when done).
-hipError_t launch_step_finish(DecodeCtl *ctl, hipStream_t s);
 
 }  // namespace itts

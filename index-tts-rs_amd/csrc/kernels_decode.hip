@@ -1,12 +1,15 @@
-// Decode-path kernels for gfx950: batch-1 dequantising GEMV with fused LayerNorm
-// prologue and bias / residual / GELU / QKV-scatter epilogues, split-K decode
-// attention over the bf16 (or fp32) KV cache, and the step embedding.
+// Decode-path kernels for gfx950: batch-1 dequantising GEMV with fused LayerNorm /
+// embedding prologues and bias / residual / GELU / QKV-scatter epilogues, split-K decode
+// attention with an in-kernel combine, and the prefill helpers (row embedding, row
+// LayerNorm, causal attention).
 //
 // GEMV layout.  A wave owns R output rows.  Row o's codes are read as 16-byte chunks
-// (16 int8 codes or 32 int4 codes) with consecutive lanes on consecutive chunks, so a
-// wave issues fully coalesced 1 KiB loads.  The group affine is folded algebraically:
+// (16 int8 codes or 32 int4 codes), consecutive lanes on consecutive chunks, so a wave
+// issues fully coalesced 1 KiB loads.  Every weight load of the block is issued before
+// the prologue (LayerNorm of the input row, or the step embedding), so the prologue runs
+// while the codes are in flight.  The group affine is folded algebraically:
 //   sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k,
-// with the per-chunk sums of x computed once per block in LDS.  All arithmetic is fp32.
+// with the per-chunk sums of x formed once per block in LDS.  All arithmetic is fp32.
 #include "kernels.h"
 
 namespace itts {
@@ -14,7 +17,7 @@ namespace itts {
 namespace {
 
 constexpr int kGemvThreads = 256;
-constexpr int kNcMax = 8;  // chunks per lane per row (K <= 8192 int8 / 16384 int4)
+constexpr int kAttnKeys = 256;  // keys per decode-attention split
 
 template <int BITS>
 __device__ inline float chunk_dot(const uint4 c, const float *xc) {
@@ -56,44 +59,79 @@ __device__ inline void store_kv(void *cache, size_t idx, float v) {
   }
 }
 
-template <int BITS, int PT, int PRO, int EPI, int KVT, int R>
+// NC: 16-byte chunks per lane per row (ceil(K / elements-per-chunk / 64)).
+template <int BITS, int PT, int PRO, int EPI, int KVT, int R, int NC>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   if (a.ctl != nullptr && a.ctl->done) return;
   extern __shared__ float smem[];
   constexpr int EPC = BITS == 8 ? 16 : 32;  // elements per 16-byte chunk
+  constexpr int XPT = NC * EPC * 64 / kGemvThreads;  // input values per thread (upper bound)
   const int K = a.ql.K, N = a.ql.N;
   const int nchunk = K / EPC;
+  const int tid = threadIdx.x;
   float *xl = smem;
   float *xsum = smem + K;
   float *red = xsum + nchunk;
 
-  if constexpr (PRO == kProNone) {
-    for (int i = threadIdx.x; i < K; i += kGemvThreads) xl[i] = a.x[i];
+  // 1. input row first: it is needed before the weights, and loads complete in issue order
+  float xr[XPT];
+  if constexpr (PRO == kProEmbedLN) {
+    const float *me = a.emb_tok + (size_t)a.ctl->tok * K;
+    const float *mp = a.emb_pos + (size_t)a.ctl->pos * K;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+      const int idx = tid + kGemvThreads * i;
+      xr[i] = idx < K ? me[idx] + mp[idx] : 0.0f;
+    }
+  } else if constexpr (PRO == kProAttn) {
+    // combine the attention splits: out[h][e] = sum_s o_s[e] e^{m_s-M} / sum_s l_s e^{m_s-M}.
+    // Stage A: per (head, split) the scaled weight e^{m_s-M}/den into LDS.
+    const int L = a.ctl != nullptr ? a.ctl->valid_len + 1 : a.attn.static_len;
+    const int S = (L + kAttnKeys - 1) / kAttnKeys;
+    const int H = a.attn.n_head, MS = a.attn.max_splits;
+    float *wts = red + 8;  // [H][S]
+    for (int h = tid; h < H; h += kGemvThreads) {
+      const float *ph = a.attn.part + (size_t)h * MS * 66;
+      float M = -INFINITY;
+      for (int s = 0; s < S; s++) M = fmaxf(M, ph[s * 66]);
+      float den = 0.0f;
+      for (int s = 0; s < S; s++) den += ph[s * 66 + 1] * __expf(ph[s * 66] - M);
+      const float inv = 1.0f / den;
+      for (int s = 0; s < S; s++) wts[h * S + s] = __expf(ph[s * 66] - M) * inv;
+    }
     __syncthreads();
+    // Stage B: the weighted sum of this thread's elements (loads issued before the weights)
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+      const int idx = tid + kGemvThreads * i;
+      float acc = 0.0f;
+      if (idx < K) {
+        const int h = idx >> 6, e = idx & 63;
+        const float *ph = a.attn.part + (size_t)h * MS * 66 + 2 + e;
+        for (int s = 0; s < S; s++) acc += ph[s * 66] * wts[h * S + s];
+      }
+      xr[i] = acc;
+    }
   } else {
-    layernorm_to_lds<kGemvThreads>(a.x, a.ln_w, a.ln_b, K, xl, red);
-    if constexpr (PRO == kProLNLN) layernorm_lds_inplace<kGemvThreads>(xl, a.ln2_w, a.ln2_b, K, red);
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+      const int idx = tid + kGemvThreads * i;
+      xr[i] = idx < K ? a.x[idx] : 0.0f;
+    }
   }
-  for (int c = threadIdx.x; c < nchunk; c += kGemvThreads) {
-    float s = 0.0f;
-#pragma unroll 8
-    for (int i = 0; i < EPC; i++) s += xl[c * EPC + i];
-    xsum[c] = s;
-  }
-  __syncthreads();
 
+  // 2. weight loads
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * (kGemvThreads / 64) + wave) * R;
   const size_t row_bytes = (size_t)K * BITS / 8;
   const int G = K / kGroup;
-
-  uint4 cw[R][kNcMax];
-  float2 pr[R][kNcMax];
+  uint4 cw[R][NC];
+  float2 pr[R][NC];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int row = row0 + r;
 #pragma unroll
-    for (int j = 0; j < kNcMax; j++) {
+    for (int j = 0; j < NC; j++) {
       const int c = lane + 64 * j;
       if (row < N && c < nchunk) {
         cw[r][j] = *reinterpret_cast<const uint4 *>(a.ql.codes + row * row_bytes + (size_t)c * 16);
@@ -104,12 +142,43 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
       }
     }
   }
+
+  // 3. prologue: the input row into LDS (waits for the input loads only), then LayerNorm
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int idx = tid + kGemvThreads * i;
+    if (idx < K) xl[idx] = xr[i];
+  }
+  if constexpr (PRO == kProEmbedLN) {
+    // x = mel_emb[tok] + mel_pos[pos] (gpt.rs:720-725); block 0 keeps it as the residual
+    if (blockIdx.x == 0) {
+#pragma unroll
+      for (int i = 0; i < XPT; i++) {
+        const int idx = tid + kGemvThreads * i;
+        if (idx < K) a.x_out[idx] = xr[i];
+      }
+    }
+  }
+  __syncthreads();
+  if constexpr (PRO == kProLN || PRO == kProLNLN || PRO == kProEmbedLN) {
+    layernorm_lds_inplace<kGemvThreads>(xl, a.ln_w, a.ln_b, K, red);
+    if constexpr (PRO == kProLNLN) layernorm_lds_inplace<kGemvThreads>(xl, a.ln2_w, a.ln2_b, K, red);
+  }
+  for (int c = threadIdx.x; c < nchunk; c += kGemvThreads) {
+    float s = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < EPC; i++) s += xl[c * EPC + i];
+    xsum[c] = s;
+  }
+  __syncthreads();
+
+  // 3. dot products, wave reduction, epilogue
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int row = row0 + r;
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kNcMax; j++) {
+    for (int j = 0; j < NC; j++) {
       const int c = lane + 64 * j;
       if (c < nchunk) {
         const float d = chunk_dot<BITS>(cw[r][j], xl + c * EPC);
@@ -139,42 +208,68 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
       }
     }
   }
+  // the head of a decode step closes the step: the cache now holds one more row
+  if (a.finish != nullptr && blockIdx.x == 0 && threadIdx.x == 0) a.finish->valid_len += 1;
 }
 
-template <int BITS, int PT, int PRO, int EPI, int KVT>
+template <int BITS, int PT, int PRO, int EPI, int KVT, int NC>
 hipError_t gemv_dispatch_r(const GemvArgs &a, hipStream_t s) {
   const int K = a.ql.K, N = a.ql.N;
   const int EPC = BITS == 8 ? 16 : 32;
-  const size_t lds = sizeof(float) * ((size_t)K + K / EPC + 8);
+  const size_t attn_wts = PRO == kProAttn ? (size_t)a.attn.n_head * a.attn.max_splits : 0;
+  const size_t lds = sizeof(float) * ((size_t)K + K / EPC + 8 + attn_wts);
   const int waves = kGemvThreads / 64;
-  // Rows per wave: 4 when that still gives >= 256 blocks, else 1.
-  if ((N + waves * 4 - 1) / (waves * 4) >= 256) {
-    const int blocks = (N + waves * 4 - 1) / (waves * 4);
-    hipLaunchKernelGGL((gemv_kernel<BITS, PT, PRO, EPI, KVT, 4>), dim3(blocks), dim3(kGemvThreads),
+  // two rows per wave when that still leaves >= 2 blocks per CU, else one
+  if ((N + waves * 2 - 1) / (waves * 2) >= 448) {
+    const int blocks = (N + waves * 2 - 1) / (waves * 2);
+    hipLaunchKernelGGL((gemv_kernel<BITS, PT, PRO, EPI, KVT, 2, NC>), dim3(blocks), dim3(kGemvThreads),
                        lds, s, a);
   } else {
     const int blocks = (N + waves - 1) / waves;
-    hipLaunchKernelGGL((gemv_kernel<BITS, PT, PRO, EPI, KVT, 1>), dim3(blocks), dim3(kGemvThreads),
+    hipLaunchKernelGGL((gemv_kernel<BITS, PT, PRO, EPI, KVT, 1, NC>), dim3(blocks), dim3(kGemvThreads),
                        lds, s, a);
   }
   return hipGetLastError();
 }
 
+template <int BITS, int PT, int PRO, int EPI, int KVT>
+hipError_t gemv_dispatch_nc(const GemvArgs &a, hipStream_t s) {
+  const int epc = BITS == 8 ? 16 : 32;
+  const int nc = (a.ql.K / epc + 63) / 64;
+  switch (nc) {
+    case 1: return gemv_dispatch_r<BITS, PT, PRO, EPI, KVT, 1>(a, s);
+    case 2: return gemv_dispatch_r<BITS, PT, PRO, EPI, KVT, 2>(a, s);
+    case 3: return gemv_dispatch_r<BITS, PT, PRO, EPI, KVT, 3>(a, s);
+    case 4:
+    case 5: return gemv_dispatch_r<BITS, PT, PRO, EPI, KVT, 5>(a, s);
+    case 6:
+    case 7:
+    case 8: return gemv_dispatch_r<BITS, PT, PRO, EPI, KVT, 8>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int BITS, int PT>
 hipError_t gemv_dispatch_pe(const GemvArgs &a, int pro, int epi, int kvt, hipStream_t s) {
-  if (pro == kProLN && epi == kEpiQKV) {
-    return kvt == kKvBf16 ? gemv_dispatch_r<BITS, PT, kProLN, kEpiQKV, kKvBf16>(a, s)
-                          : gemv_dispatch_r<BITS, PT, kProLN, kEpiQKV, kKvF32>(a, s);
+  if (epi == kEpiQKV && (pro == kProLN || pro == kProEmbedLN)) {
+    if (pro == kProLN)
+      return kvt == kKvBf16 ? gemv_dispatch_nc<BITS, PT, kProLN, kEpiQKV, kKvBf16>(a, s)
+                            : gemv_dispatch_nc<BITS, PT, kProLN, kEpiQKV, kKvF32>(a, s);
+    return kvt == kKvBf16 ? gemv_dispatch_nc<BITS, PT, kProEmbedLN, kEpiQKV, kKvBf16>(a, s)
+                          : gemv_dispatch_nc<BITS, PT, kProEmbedLN, kEpiQKV, kKvF32>(a, s);
   }
-  if (pro == kProNone && epi == kEpiResid) return gemv_dispatch_r<BITS, PT, kProNone, kEpiResid, 0>(a, s);
-  if (pro == kProLN && epi == kEpiGelu) return gemv_dispatch_r<BITS, PT, kProLN, kEpiGelu, 0>(a, s);
-  if (pro == kProLNLN && epi == kEpiStore) return gemv_dispatch_r<BITS, PT, kProLNLN, kEpiStore, 0>(a, s);
-  if (pro == kProNone && epi == kEpiStore) return gemv_dispatch_r<BITS, PT, kProNone, kEpiStore, 0>(a, s);
+  if (pro == kProNone && epi == kEpiResid) return gemv_dispatch_nc<BITS, PT, kProNone, kEpiResid, 0>(a, s);
+  if (pro == kProAttn && epi == kEpiResid) return gemv_dispatch_nc<BITS, PT, kProAttn, kEpiResid, 0>(a, s);
+  if (pro == kProLN && epi == kEpiGelu) return gemv_dispatch_nc<BITS, PT, kProLN, kEpiGelu, 0>(a, s);
+  if (pro == kProLNLN && epi == kEpiStore) return gemv_dispatch_nc<BITS, PT, kProLNLN, kEpiStore, 0>(a, s);
+  if (pro == kProNone && epi == kEpiStore) return gemv_dispatch_nc<BITS, PT, kProNone, kEpiStore, 0>(a, s);
   return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------------
-// Attention
+// Decode attention: grid (head, split), 256 keys per split (4 waves x 64 keys).  Each
+// block writes its partial (max, denominator, 64 unnormalised outputs); the c_proj GEMV
+// that consumes the attention output combines the partials in its prologue.
 // ---------------------------------------------------------------------------------
 
 template <int KVT>
@@ -204,18 +299,129 @@ __device__ inline void load_row64(const void *base, size_t row, float *out) {
   }
 }
 
+// 8 consecutive elements of row `row` starting at column c0.
 template <int KVT>
-__device__ inline float load_elem(const void *base, size_t idx) {
+__device__ inline void load_row8(const void *base, size_t row, int c0, float *out) {
   if constexpr (KVT == kKvBf16) {
-    return __uint_as_float((uint32_t) static_cast<const uint16_t *>(base)[idx] << 16);
+    const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      out[2 * j] = __uint_as_float(w[j] << 16);
+      out[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
   } else {
-    return static_cast<const float *>(base)[idx];
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + row * 64 + c0);
+    const float4 f0 = p[0], f1 = p[1];
+    out[0] = f0.x; out[1] = f0.y; out[2] = f0.z; out[3] = f0.w;
+    out[4] = f1.x; out[5] = f1.y; out[6] = f1.z; out[7] = f1.w;
   }
 }
 
-// One wave: online-softmax attention of query q (64 values, global) over keys j0..j1-1
-// of one head's cache slice (rows of 64).  Returns the running max m, the denominator
-// l and, in lane e, the unnormalised output o[e].
+template <int KVT>
+__device__ inline const void *head_base(const void *c, size_t off) {
+  return KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(c) + off)
+                        : (const void *)(static_cast<const float *>(c) + off);
+}
+
+struct AttnShared {
+  float p[4][64];      // probabilities per wave
+  float o[4][64];      // per-wave unnormalised outputs
+  float m[4], l[4];
+};
+
+template <int KVT>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const void *kc, const void *vc,
+                                                          int max_seq, const DecodeCtl *ctl, int static_len,
+                                                          float *part) {
+  if (ctl != nullptr && ctl->done) return;
+  __shared__ AttnShared sh;
+  const int h = blockIdx.x, s = blockIdx.y;
+  const int L = ctl != nullptr ? ctl->valid_len + 1 : static_len;
+  const int S = (L + kAttnKeys - 1) / kAttnKeys;  // active splits
+  if (s >= S) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const size_t hb = (size_t)h * max_seq * 64;
+  const void *kh = head_base<KVT>(kc, hb);
+  const void *vh = head_base<KVT>(vc, hb);
+  const int jw = s * kAttnKeys + wave * 64;  // this wave's first key
+  const int j = jw + lane;
+  const int kg = lane >> 3, dg = lane & 7;   // P.V layout: key group, 8-wide dim group
+
+  // K row of this lane's key and the V slices of its P.V share, all loads in flight at once
+  float kr[64];
+  if (j < L) load_row64<KVT>(kh, (size_t)j, kr);
+  float v8[8][8];
+#pragma unroll
+  for (int kk = 0; kk < 8; kk++) {
+    const int key = jw + kg + 8 * kk;
+    if (key < L) {
+      load_row8<KVT>(vh, (size_t)key, dg * 8, v8[kk]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v8[kk][e] = 0.0f;
+    }
+  }
+  float sc = -INFINITY;
+  if (j < L) {
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + h * 64);
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float4 qv = q4[i];
+      dot += qv.x * kr[4 * i] + qv.y * kr[4 * i + 1] + qv.z * kr[4 * i + 2] + qv.w * kr[4 * i + 3];
+    }
+    sc = dot * 0.125f;
+  }
+  const float mw = wave_max(sc);
+  const float p = (j < L) ? __expf(sc - mw) : 0.0f;
+  const float lw = wave_sum(p);
+  sh.p[wave][lane] = p;
+  __syncthreads();
+  float o8[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) o8[e] = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < 8; kk++) {
+    const float pk = sh.p[wave][kg + 8 * kk];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o8[e] += pk * v8[kk][e];
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) o8[e] += __shfl_xor(o8[e], off, 64);
+  }
+  if (kg == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) sh.o[wave][dg * 8 + e] = o8[e];
+  }
+  if (lane == 0) {
+    sh.m[wave] = mw;
+    sh.l[wave] = lw;
+  }
+  __syncthreads();
+  // block partial: the four waves merged
+  if (wave == 0) {
+    float *mine = part + ((size_t)h * gridDim.y + s) * 66;
+    float M = -INFINITY;
+    for (int w = 0; w < 4; w++) M = fmaxf(M, sh.m[w]);
+    float lsum = 0.0f, osum = 0.0f;
+    for (int w = 0; w < 4; w++) {
+      if (sh.m[w] == -INFINITY) continue;
+      const float f = __expf(sh.m[w] - M);
+      lsum += sh.l[w] * f;
+      osum += sh.o[w][lane] * f;
+    }
+    mine[2 + lane] = osum;
+    if (lane == 0) {
+      mine[0] = M;
+      mine[1] = lsum;
+    }
+  }
+}
+
+// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows).
 template <int KVT>
 __device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
                                   float &m, float &l, float &o, float *p_lds) {
@@ -252,62 +458,15 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
     __syncthreads();
     o *= corr;
     const int cnt = min(64, j1 - t0);
-    for (int jj = 0; jj < cnt; jj++) o += p_lds[jj] * load_elem<KVT>(vh, (size_t)(t0 + jj) * 64 + lane);
+    for (int jj = 0; jj < cnt; jj++) {
+      const size_t idx = (size_t)(t0 + jj) * 64 + lane;
+      const float v = KVT == kKvBf16 ? __uint_as_float((uint32_t) static_cast<const uint16_t *>(vh)[idx] << 16)
+                                     : static_cast<const float *>(vh)[idx];
+      o += p_lds[jj] * v;
+    }
     __syncthreads();
     m = mn;
   }
-}
-
-template <int KVT>
-__global__ __launch_bounds__(64) void attn_decode_split_kernel(const float *q, const void *kc,
-                                                               const void *vc, int max_seq,
-                                                               const DecodeCtl *ctl, int static_len,
-                                                               int chunk, float *part) {
-  if (ctl != nullptr && ctl->done) return;
-  __shared__ float p_lds[64];
-  const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y;
-  const int L = ctl != nullptr ? ctl->valid_len + 1 : static_len;
-  const int j0 = s * chunk, j1 = min(L, j0 + chunk);
-  float *out = part + ((size_t)h * S + s) * 66;
-  const int lane = threadIdx.x;
-  if (j0 >= L) {
-    if (lane == 0) {
-      out[0] = -INFINITY;
-      out[1] = 0.0f;
-    }
-    out[2 + lane] = 0.0f;
-    return;
-  }
-  const size_t hb = (size_t)h * max_seq * 64;
-  const void *kh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(kc) + hb)
-                                  : (const void *)(static_cast<const float *>(kc) + hb);
-  const void *vh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(vc) + hb)
-                                  : (const void *)(static_cast<const float *>(vc) + hb);
-  float m, l, o;
-  attn_range<KVT>(q + h * 64, kh, vh, j0, j1, m, l, o, p_lds);
-  if (lane == 0) {
-    out[0] = m;
-    out[1] = l;
-  }
-  out[2 + lane] = o;
-}
-
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, int S,
-                                                          const DecodeCtl *ctl, float *out) {
-  if (ctl != nullptr && ctl->done) return;
-  const int h = blockIdx.x, e = threadIdx.x;
-  const float *p = part + (size_t)h * S * 66;
-  float M = -INFINITY;
-  for (int s = 0; s < S; s++) M = fmaxf(M, p[s * 66]);
-  float den = 0.0f, num = 0.0f;
-  for (int s = 0; s < S; s++) {
-    const float ms = p[s * 66];
-    if (ms == -INFINITY) continue;
-    const float w = __expf(ms - M);
-    den += p[s * 66 + 1] * w;
-    num += p[s * 66 + 2 + e] * w;
-  }
-  out[h * 64 + e] = num / den;
 }
 
 template <int KVT>
@@ -317,26 +476,15 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int ba
   __shared__ float p_lds[64];
   const int h = blockIdx.x, t = blockIdx.y;
   const size_t hb = (size_t)h * max_seq * 64;
-  const void *kh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(kc) + hb)
-                                  : (const void *)(static_cast<const float *>(kc) + hb);
-  const void *vh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(vc) + hb)
-                                  : (const void *)(static_cast<const float *>(vc) + hb);
   float m, l, o;
-  attn_range<KVT>(q + (size_t)t * d + h * 64, kh, vh, 0, base + t + 1, m, l, o, p_lds);
+  attn_range<KVT>(q + (size_t)t * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), 0, base + t + 1,
+                  m, l, o, p_lds);
   out[(size_t)t * d + h * 64 + threadIdx.x] = o / l;
 }
 
 // ---------------------------------------------------------------------------------
-// Embeddings and LayerNorm rows
+// Prefill embeddings and LayerNorm rows
 // ---------------------------------------------------------------------------------
-
-__global__ __launch_bounds__(256) void embed_step_kernel(const float *mel_emb, const float *mel_pos,
-                                                         const DecodeCtl *ctl, int d, float *x) {
-  if (ctl->done) return;
-  const float *me = mel_emb + (size_t)ctl->tok * d;
-  const float *mp = mel_pos + (size_t)ctl->pos * d;
-  for (int i = threadIdx.x; i < d; i += 256) x[i] = me[i] + mp[i];
-}
 
 __global__ __launch_bounds__(256) void embed_rows_kernel(const EmbedRow *rows, const float *conds,
                                                          const float *text_emb, const float *lang_row,
@@ -366,16 +514,13 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, const floa
   for (int i = threadIdx.x; i < d; i += 256) y[(size_t)blockIdx.x * d + i] = smem[i];
 }
 
-__global__ void step_finish_kernel(DecodeCtl *ctl) {
-  if (!ctl->done) ctl->valid_len += 1;
-}
-
 }  // namespace
 
 hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi, int kvt,
                        hipStream_t s) {
   const int epc = bits == 8 ? 16 : 32;
-  if (a.ql.K % kGroup != 0 || a.ql.K / epc > 64 * kNcMax) return hipErrorInvalidValue;
+  if (a.ql.K % kGroup != 0 || a.ql.K / epc > 64 * 8) return hipErrorInvalidValue;
+  if (pro == kProEmbedLN && a.ctl == nullptr) return hipErrorInvalidValue;
   if (bits == 8) {
     return ptype == kParamF16 ? gemv_dispatch_pe<8, kParamF16>(a, pro, epi, kvt, s)
                               : gemv_dispatch_pe<8, kParamF32>(a, pro, epi, kvt, s);
@@ -387,18 +532,19 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
   return hipErrorInvalidValue;
 }
 
+int attn_decode_max_splits(int max_seq) { return (max_seq + kAttnKeys - 1) / kAttnKeys; }
+
 hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, int n_head,
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,
-                              int max_splits, int chunk, float *out, int kvt, hipStream_t s) {
-  dim3 grid(n_head, max_splits);
+                              int kvt, hipStream_t s) {
+  dim3 grid(n_head, attn_decode_max_splits(max_seq));
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_decode_split_kernel<kKvBf16>, grid, dim3(64), 0, s, q, kc, vc, max_seq,
-                       ctl, static_len, chunk, part);
+    hipLaunchKernelGGL(attn_decode_kernel<kKvBf16>, grid, dim3(256), 0, s, q, kc, vc, max_seq, ctl, static_len,
+                       part);
   } else {
-    hipLaunchKernelGGL(attn_decode_split_kernel<kKvF32>, grid, dim3(64), 0, s, q, kc, vc, max_seq,
-                       ctl, static_len, chunk, part);
+    hipLaunchKernelGGL(attn_decode_kernel<kKvF32>, grid, dim3(256), 0, s, q, kc, vc, max_seq, ctl, static_len,
+                       part);
   }
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(n_head), dim3(64), 0, s, part, max_splits, ctl, out);
   return hipGetLastError();
 }
 
@@ -407,18 +553,10 @@ hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, 
   dim3 grid(n_head, T);
   const int d = n_head * 64;
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvBf16>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d,
-                       out);
+    hipLaunchKernelGGL(attn_prefill_kernel<kKvBf16>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
   } else {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvF32>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d,
-                       out);
+    hipLaunchKernelGGL(attn_prefill_kernel<kKvF32>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_embed_step(const float *mel_emb, const float *mel_pos, const DecodeCtl *ctl,
-                             int d, float *x, hipStream_t s) {
-  hipLaunchKernelGGL(embed_step_kernel, dim3(1), dim3(256), 0, s, mel_emb, mel_pos, ctl, d, x);
   return hipGetLastError();
 }
 
@@ -434,11 +572,6 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
                           float *y, hipStream_t s) {
   hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, d, y);
-  return hipGetLastError();
-}
-
-hipError_t launch_step_finish(DecodeCtl *ctl, hipStream_t s) {
-  hipLaunchKernelGGL(step_finish_kernel, dim3(1), dim3(1), 0, s, ctl);
   return hipGetLastError();
 }
 

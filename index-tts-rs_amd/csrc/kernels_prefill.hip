@@ -196,6 +196,7 @@ hipError_t gemm_dispatch(const GemmArgs &a, int epi, int kvt, hipStream_t s) {
 // out[o][k] = float(q) * s then + b: two roundings, no contraction.
 template <int BITS, int PT>
 __global__ __launch_bounds__(256) void dequant_kernel(DevQL ql, float *out) {
+#pragma clang fp contract(off)
   const size_t total = (size_t)ql.N * ql.K;
   const int G = ql.K / kGroup;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(DevQL ql, float *out) {
       q = (k & 1) ? (b >> 4) : (b & 0xf);
     }
     const float2 sb = load_param<PT>(ql.params, (size_t)o * G + k / kGroup);
-    out[i] = __fadd_rn(__fmul_rn((float)q, sb.x), sb.y);
+    out[i] = add_rn(mul_rn((float)q, sb.x), sb.y);
   }
 }
 

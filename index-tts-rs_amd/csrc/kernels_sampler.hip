@@ -16,6 +16,10 @@
 // probabilities' prefix sums, the top-p cut and the draw.
 #include "kernels.h"
 
+// Every multiply and add in this file rounds on its own (no FMA contraction), as the
+// reference's scalar Rust code does; the exponential uses explicit fmaf where intended.
+#pragma clang fp contract(off)
+
 namespace itts {
 
 namespace {
@@ -29,7 +33,7 @@ __device__ inline float sampler_expf(float x) {
   if (x != x) return x;
   if (x > 88.72283935546875f) return INFINITY;
   if (x < -87.33654022216797f) return 0.0f;
-  const float n = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
+  const float n = __builtin_rintf(mul_rn(x, 1.44269502162933349609375f));
   float r = __builtin_fmaf(-n, 0.693145751953125f, x);
   r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
   float p = 1.98412698412698413e-4f;
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
       x = logits[i];
       if (mask_stop && i == stop_tok) x = -INFINITY;
       if (p.apply_penalty && (i >> 6) < kSeenWords && ((seen[i >> 6] >> (i & 63)) & 1ull)) {
-        x = x < 0.0f ? __fmul_rn(x, p.penalty) : __fdiv_rn(x, p.penalty);
+        x = x < 0.0f ? mul_rn(x, p.penalty) : div_rn(x, p.penalty);
       }
       if (mode == 0) logits[i] = x;
     }
@@ -152,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
     for (int e = 0; e < kPerThread; e++) {
       const int i = i0 + e;
       const bool live = e < E && i < n;
-      const float s = is_finite(v[e]) ? __fmul_rn(v[e], p.inv_temp) : -INFINITY;
+      const float s = is_finite(v[e]) ? mul_rn(v[e], p.inv_temp) : -INFINITY;
       v[e] = s;
       key[e] = live ? order_key(s) : 0u;  // padding sorts below -inf (key 0x007fffff)
     }
@@ -264,35 +268,35 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
       const uint64_t e = sk[i];
       const float vi = key_value((uint32_t)(e >> 32));
       const uint32_t id = 0xffffffffu - (uint32_t)e;
-      const float pi = is_finite(vi) ? sampler_expf(__fsub_rn(vi, mx)) : 0.0f;
+      const float pi = is_finite(vi) ? sampler_expf(sub_rn(vi, mx)) : 0.0f;
       sk[i] = ((uint64_t)__float_as_uint(pi) << 32) | id;
     }
     __syncthreads();
     if (tid == 0) {
       float prob_sum = 0.0f;
-      for (int i = 0; i < k; i++) prob_sum = __fadd_rn(prob_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
+      for (int i = 0; i < k; i++) prob_sum = add_rn(prob_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
       int32_t tok = (int32_t)(uint32_t)sk[0];
       if (prob_sum > 0.0f && is_finite(prob_sum)) {
         float cum = 0.0f;
         int active = k;
         for (int i = 0; i < k; i++) {
-          const float norm = __fdiv_rn(__uint_as_float((uint32_t)(sk[i] >> 32)), prob_sum);
+          const float norm = div_rn(__uint_as_float((uint32_t)(sk[i] >> 32)), prob_sum);
           if (i > 0 && cum > p.top_p) {
             active = i;
             break;
           }
-          cum = __fadd_rn(cum, norm);
+          cum = add_rn(cum, norm);
         }
         float active_sum = 0.0f;
-        for (int i = 0; i < active; i++) active_sum = __fadd_rn(active_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
+        for (int i = 0; i < active; i++) active_sum = add_rn(active_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
         if (active_sum > 0.0f && is_finite(active_sum)) {
           const uint32_t upper = (uint32_t)(splitmix_next(rng) >> 40);
-          const float u = __fmul_rn((float)upper, 1.0f / 16777216.0f);
-          const float draw = __fmul_rn(u, active_sum);
+          const float u = mul_rn((float)upper, 1.0f / 16777216.0f);
+          const float draw = mul_rn(u, active_sum);
           float accp = 0.0f;
           tok = (int32_t)(uint32_t)sk[active - 1];
           for (int i = 0; i < active; i++) {
-            accp = __fadd_rn(accp, __uint_as_float((uint32_t)(sk[i] >> 32)));
+            accp = add_rn(accp, __uint_as_float((uint32_t)(sk[i] >> 32)));
             if (draw <= accp) {
               tok = (int32_t)(uint32_t)sk[i];
               break;

@@ -42,8 +42,6 @@ itts_status set_error(itts_status st, const char *fmt, ...) {
                        __FILE__, __LINE__, #expr);                                       \
   } while (0)
 
-constexpr int kAttnChunk = 64;  // keys per decode-attention split
-
 struct DevBuf {
   void *p = nullptr;
   size_t bytes = 0;
@@ -100,9 +98,17 @@ struct QLHost {
   int N = 0, K = 0;
 };
 
+// A decoder is shared by its KV caches: each cache holds a reference, so destroying the
+// decoder while caches are alive (in any order) never leaves a cache pointing at freed
+// memory; the object goes when the last of them is released.
 struct itts_gpt {
   itts_config cfg{};
   hipStream_t stream = nullptr;
+  int refs = 1;
+  bool user_released = false;
+  // Decode iterations replay a captured graph; ITTS_NO_GRAPH=1 enqueues the same
+  // kernels directly (for tools that cannot follow graph launches).
+  bool use_graph = true;
   int max_cond = 64;
   DevBuf text_emb, lang_emb, mel_emb, mel_pos, text_pos;
   std::vector<DevBuf> ln;  // ln1_w, ln1_b, ln2_w, ln2_b per layer, then ln_f, final_norm
@@ -135,6 +141,10 @@ struct itts_kv {
   hipGraph_t graph = nullptr;
   DevSampling gkey{};
   bool have_graph = false;
+  // timing of the last generate call
+  hipEvent_t ev_t[3] = {nullptr, nullptr, nullptr};
+  itts_timing timing{};
+  bool timing_valid = false;
   size_t layer_elems() const { return (size_t)gpt->cfg.n_head * max_seq * 64; }
   void *k_layer(int l) const {
     return static_cast<char *>(k.p) + layer_elems() * l * (kvt == kKvBf16 ? 2 : 4);
@@ -143,6 +153,8 @@ struct itts_kv {
     return static_cast<char *>(v.p) + layer_elems() * l * (kvt == kKvBf16 ? 2 : 4);
   }
   ~itts_kv() {
+    for (hipEvent_t e : ev_t)
+      if (e) (void)hipEventDestroy(e);
     if (gexec) (void)hipGraphExecDestroy(gexec);
     if (graph) (void)hipGraphDestroy(graph);
     if (host_ctl) (void)hipHostFree(host_ctl);
@@ -264,8 +276,7 @@ itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
   const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
   DecodeCtl *ctl = kv->ctl.as<DecodeCtl>();
-  float *x = g->x.as<float>(), *q = g->q.as<float>(), *a = g->a.as<float>(), *f = g->f.as<float>();
-  HIP_TRY(launch_embed_step(g->mel_emb.as<float>(), g->mel_pos.as<float>(), ctl, d, x, s));
+  float *x = g->x.as<float>(), *q = g->q.as<float>(), *f = g->f.as<float>();
   for (int l = 0; l < c.n_layer; l++) {
     const DevLayer &L = g->layers[l];
     GemvArgs ga{};
@@ -275,15 +286,20 @@ itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
     ga.ln_b = L.ln1_b;
     ga.qkv = QkvDst{q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
     ga.ctl = ctl;
-    HIP_TRY(launch_gemv(ga, bits, pt, kProLN, kEpiQKV, kv->kvt, s));
+    if (l == 0) {  // the step embedding is the prologue of layer 0's QKV projection
+      ga.emb_tok = g->mel_emb.as<float>();
+      ga.emb_pos = g->mel_pos.as<float>();
+      ga.x_out = x;
+    }
+    HIP_TRY(launch_gemv(ga, bits, pt, l == 0 ? kProEmbedLN : kProLN, kEpiQKV, kv->kvt, s));
     HIP_TRY(launch_attn_decode(q, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, ctl, 0,
-                               kv->part.as<float>(), kv->splits, kAttnChunk, a, kv->kvt, s));
+                               kv->part.as<float>(), kv->kvt, s));
     ga = GemvArgs{};
     ga.ql = L.proj;
-    ga.x = a;
+    ga.attn = AttnPartials{kv->part.as<float>(), c.n_head, kv->splits, 0};
     ga.y = x;
     ga.ctl = ctl;
-    HIP_TRY(launch_gemv(ga, bits, pt, kProNone, kEpiResid, kv->kvt, s));
+    HIP_TRY(launch_gemv(ga, bits, pt, kProAttn, kEpiResid, kv->kvt, s));
     ga = GemvArgs{};
     ga.ql = L.fc;
     ga.x = x;
@@ -308,8 +324,8 @@ itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
   ha.ln2_b = g->fn_b.as<float>();
   ha.y = g->logits.as<float>();
   ha.ctl = ctl;
+  ha.finish = ctl;
   HIP_TRY(launch_gemv(ha, bits, pt, kProLNLN, kEpiStore, kv->kvt, s));
-  HIP_TRY(launch_step_finish(ctl, s));
   return ITTS_OK;
 }
 
@@ -463,6 +479,7 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
   if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess)
     return fail(set_error(ITTS_E_DEVICE, "hipStreamCreate failed"));
   if (sampler_init() != hipSuccess) return fail(set_error(ITTS_E_DEVICE, "sampler LDS attribute failed"));
+  if (const char *ng = getenv("ITTS_NO_GRAPH")) g->use_graph = !(ng[0] == '1' && ng[1] == '\0');
   struct {
     const float *p;
     const char *name;
@@ -526,13 +543,19 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
   return ITTS_OK;
 }
 
-void itts_gpt_destroy(itts_gpt *gpt) {
-  if (!gpt) return;
+static void gpt_release(itts_gpt *gpt) {
+  if (--gpt->refs > 0) return;
   if (gpt->stream) {
     (void)hipStreamSynchronize(gpt->stream);
     (void)hipStreamDestroy(gpt->stream);
   }
   delete gpt;
+}
+
+void itts_gpt_destroy(itts_gpt *gpt) {
+  if (!gpt || gpt->user_released) return;
+  gpt->user_released = true;
+  gpt_release(gpt);
 }
 
 int32_t itts_gpt_num_layers(const itts_gpt *gpt) { return gpt ? gpt->cfg.n_layer : 0; }
@@ -550,7 +573,7 @@ itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, 
   kv->kvt = kv_dtype == ITTS_BF16 ? kKvBf16 : kKvF32;
   const size_t es = kv->kvt == kKvBf16 ? 2 : 4;
   const size_t n = (size_t)gpt->cfg.n_layer * kv->layer_elems();
-  kv->splits = (max_seq + kAttnChunk - 1) / kAttnChunk;
+  kv->splits = attn_decode_max_splits(max_seq);
   if (kv->k.ensure(n * es) || kv->v.ensure(n * es) || kv->ctl.ensure(sizeof(DecodeCtl)) ||
       kv->part.ensure(sizeof(float) * (size_t)gpt->cfg.n_head * kv->splits * 66) ||
       kv->codes.ensure(sizeof(int32_t) * 2048) ||
@@ -564,14 +587,17 @@ itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, 
     delete kv;
     return set_error(ITTS_E_DEVICE, "KV cache initialisation failed");
   }
+  gpt->refs += 1;
   *out = kv;
   return ITTS_OK;
 }
 
 void itts_kv_destroy(itts_kv *kv) {
   if (!kv) return;
-  if (kv->gpt && kv->gpt->stream) (void)hipStreamSynchronize(kv->gpt->stream);
+  itts_gpt *gpt = kv->gpt;
+  (void)hipStreamSynchronize(gpt->stream);
   delete kv;
+  gpt_release(gpt);
 }
 
 void itts_kv_reset(itts_kv *kv) {
@@ -721,10 +747,15 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
                      "codes fill the capacity)");
   if (codes_cap < max_steps) return set_error(ITTS_E_VALIDATION, "codes_out: capacity %d < %d", codes_cap, max_steps);
   if (prompt->min_codes < 0) return set_error(ITTS_E_VALIDATION, "min_codes: negative");
+  kv->timing_valid = false;
+  for (hipEvent_t &ev : kv->ev_t)
+    if (!ev) HIP_TRY(hipEventCreate(&ev));
+  HIP_TRY(hipEventRecord(kv->ev_t[0], gpt->stream));
   int T = 0;
   itts_status st = run_prefill(gpt, kv, prompt->text_tokens, prompt->n_text, prompt->conds, prompt->n_cond,
                                prompt->lang_id, prompt->prior_codes, prompt->n_prior, &T);
   if (st) return st;
+  HIP_TRY(hipEventRecord(kv->ev_t[1], gpt->stream));
   // Sample s is followed by a step that writes cache row T + s; the reference fails that
   // step with a KV-capacity error once T + s + 1 > max_seq (gpt.rs:157-165).  The device
   // loop therefore runs at most max_seq - T + 1 samples and reports the overflow if it
@@ -746,8 +777,15 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   if ((st = write_ctl(kv, h))) return st;
 
   const DevSampling ds = to_dev_sampling(*p, c.mel_vocab);
+  auto enqueue_iteration = [&]() -> itts_status {
+    hipError_t le = launch_sampler(gpt->logits.as<float>(), c.mel_vocab, nullptr, ds, nullptr, nullptr,
+                                   kv->ctl.as<DecodeCtl>(), kv->codes.as<int32_t>(), c.mel_vocab - 1, 1,
+                                   gpt->stream);
+    if (le != hipSuccess) return set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
+    return enqueue_decode_step(gpt, kv);
+  };
   // capture one decode iteration (sample, then step) once per cache and parameters
-  if (!kv->have_graph || !same_sampling(kv->gkey, ds)) {
+  if (gpt->use_graph && (!kv->have_graph || !same_sampling(kv->gkey, ds))) {
     if (kv->gexec) {
       (void)hipGraphExecDestroy(kv->gexec);
       kv->gexec = nullptr;
@@ -759,11 +797,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     kv->have_graph = false;
     HIP_TRY(hipStreamSynchronize(gpt->stream));
     HIP_TRY(hipStreamBeginCapture(gpt->stream, hipStreamCaptureModeThreadLocal));
-    hipError_t le = launch_sampler(gpt->logits.as<float>(), c.mel_vocab, nullptr, ds, nullptr, nullptr,
-                                   kv->ctl.as<DecodeCtl>(), kv->codes.as<int32_t>(), c.mel_vocab - 1, 1,
-                                   gpt->stream);
-    itts_status es = le == hipSuccess ? enqueue_decode_step(gpt, kv)
-                                      : set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
+    itts_status es = enqueue_iteration();
     hipGraph_t graph = nullptr;
     hipError_t ce = hipStreamEndCapture(gpt->stream, &graph);
     if (es) {
@@ -792,8 +826,12 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   };
   auto launch_batch = [&](int which) -> hipError_t {
     for (int i = 0; i < batch; i++) {
-      hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
-      if (e != hipSuccess) return e;
+      if (gpt->use_graph) {
+        hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
+        if (e != hipSuccess) return e;
+      } else if (enqueue_iteration() != ITTS_OK) {
+        return hipErrorLaunchFailure;
+      }
     }
     hipError_t e = hipMemcpyAsync(slot[which], kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost,
                                   gpt->stream);
@@ -816,6 +854,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     if (e != hipSuccess) break;
     if (slot[i & 1]->done || i + 1 >= nb_total) break;
   }
+  if (e == hipSuccess) e = hipEventRecord(kv->ev_t[2], gpt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(gpt->stream);
   cleanup();
   HIP_TRY(e);
@@ -823,6 +862,12 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   HIP_TRY(hipMemcpy(&fin, kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost));
   if (!fin.done) return set_error(ITTS_E_INTERNAL, "generation did not reach its end");
   kv->valid_len = fin.valid_len;
+  HIP_TRY(hipEventElapsedTime(&kv->timing.prefill_ms, kv->ev_t[0], kv->ev_t[1]));
+  HIP_TRY(hipEventElapsedTime(&kv->timing.decode_ms, kv->ev_t[1], kv->ev_t[2]));
+  kv->timing.prefill_rows = T;
+  kv->timing.decode_steps = fin.valid_len - T;
+  kv->timing.samples = fin.step;
+  kv->timing_valid = true;
   if (dev_steps < max_steps && fin.n_codes == dev_steps)
     return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
                      kv->max_seq + 1, kv->max_seq);
@@ -830,6 +875,13 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   *n_codes = fin.n_codes;
   *rng_state = fin.rng;
   kv->valid_len = fin.valid_len;
+  return ITTS_OK;
+}
+
+itts_status itts_kv_last_timing(const itts_kv *kv, itts_timing *out) {
+  if (!kv || !out) return set_error(ITTS_E_VALIDATION, "timing: null argument");
+  if (!kv->timing_valid) return set_error(ITTS_E_VALIDATION, "timing: no completed generate call on this cache");
+  *out = kv->timing;
   return ITTS_OK;
 }
 

@@ -101,7 +101,13 @@ class itts_code_prompt(C.Structure):
                 ("n_prior", C.c_int32), ("min_codes", C.c_int32)]
 
 
+class itts_timing(C.Structure):
+    _fields_ = [("prefill_ms", C.c_float), ("decode_ms", C.c_float), ("prefill_rows", C.c_int32),
+                ("decode_steps", C.c_int32), ("samples", C.c_int32)]
+
+
 _SIGS = {
+    "itts_kv_last_timing": (C.c_int, [C.c_void_p, C.POINTER(itts_timing)]),
     "itts_version": (C.c_char_p, []),
     "itts_last_error": (C.c_char_p, []),
     "itts_config_default": (itts_config, []),
@@ -246,9 +252,10 @@ class Gpt:
 
     def __init__(self, weights):
         self._weights = weights  # keeps host arrays referenced by the C struct alive
-        cw = weights.to_itts()
+        cw, keep = weights.to_itts()
         h = C.c_void_p()
         _check(lib.itts_gpt_create(C.byref(cw), C.byref(h)))
+        del keep  # the library has copied every tensor to the device
         self._h = h
         self.cfg = weights.cfg
 
@@ -335,6 +342,11 @@ class KvCache:
 
     def max_seq(self) -> int:
         return lib.itts_kv_max_seq(self._h)
+
+    def last_timing(self) -> dict:
+        t = itts_timing()
+        _check(lib.itts_kv_last_timing(self._h, C.byref(t)))
+        return {f: getattr(t, f) for f, _ in itts_timing._fields_}
 
     def read(self, layer: int, which_v: bool) -> np.ndarray:
         cfg = self.gpt.cfg

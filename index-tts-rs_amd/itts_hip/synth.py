@@ -12,7 +12,7 @@ the weights are identical on every host with the same numpy.
 from __future__ import annotations
 
 import ctypes as C
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -71,7 +71,6 @@ class ModelWeights:
     fn_w: np.ndarray
     fn_b: np.ndarray
     head: QLinear
-    _keep: list = field(default_factory=list, repr=False)
 
     def weight_bytes_per_step(self) -> int:
         """Bytes of quantized weights + group params + biases + LN read by one decode step."""
@@ -84,7 +83,9 @@ class ModelWeights:
         total += 2 * d * 4                           # the two embedding rows
         return total
 
-    def to_itts(self) -> itts_weights:
+    def to_itts(self):
+        """(itts_weights, keep-alive): the struct points into this object's arrays and into
+        the returned layer array, which the caller must keep referenced."""
         c = itts_config(**{k: int(self.cfg[k]) for k in (
             "n_layer", "d_model", "n_head", "d_ffn", "mel_vocab", "text_vocab", "lang_vocab",
             "mel_pos_len", "text_pos_len", "quant_bits", "param_dtype")})
@@ -93,13 +94,12 @@ class ModelWeights:
             arr[i] = itts_layer_weights(L.ln1_w.ctypes.data, L.ln1_b.ctypes.data, L.c_attn.to_c(),
                                         L.c_proj.to_c(), L.ln2_w.ctypes.data, L.ln2_b.ctypes.data,
                                         L.c_fc.to_c(), L.mlp_c_proj.to_c())
-        self._keep.append(arr)
         w = itts_weights(c, self.text_emb.ctypes.data, self.lang_emb.ctypes.data,
                          self.mel_emb.ctypes.data, self.mel_pos.ctypes.data,
                          self.text_pos.ctypes.data, C.cast(arr, C.POINTER(itts_layer_weights)),
                          self.ln_f_w.ctypes.data, self.ln_f_b.ctypes.data, self.fn_w.ctypes.data,
                          self.fn_b.ctypes.data, self.head.to_c())
-        return w
+        return w, arr
 
 
 class _Streams:

@@ -125,6 +125,21 @@ def test_generate_max_steps_clamp(model):
     assert len(codes) == room
 
 
+def test_cache_outlives_decoder():
+    """Destroying the decoder before its caches must be safe (caches hold a reference)."""
+    say("[gpu] cache outlives decoder")
+    W = synth.make_weights(synth.TINY_CONFIG, seed=4, init="rich")
+    g = H.Gpt(W)
+    pr = synth.make_prompt(W.cfg, 3, 5, seed=1)
+    kv1 = g.kv_cache(64)
+    kv2 = g.kv_cache(64)
+    g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv1)
+    g.close()
+    assert kv1.valid_len() == 3 + 5 + 3
+    kv1.close()
+    kv2.close()
+
+
 def test_validation_and_capacity_errors(model):
     W, g, _ = model
     say("[gpu] validation errors")
