@@ -106,6 +106,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--decode", default="auto", choices=["auto", "multi", "persistent"],
+                    help="decode-step implementation (auto: persistent where supported)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the decoder runs one sequence per GPU and this "
@@ -124,7 +126,11 @@ def main():
     print(f"[bench] weights generated in {time.perf_counter() - t0:.1f}s "
           f"({weight_bytes / 1e6:.1f} MB per decode step)", file=sys.stderr, flush=True)
     g = H.Gpt(W)
+    g.set_decode_path({"auto": H.ITTS_DECODE_AUTO, "multi": H.ITTS_DECODE_MULTI,
+                       "persistent": H.ITTS_DECODE_PERSISTENT}[args.decode])
     kv = g.kv_cache(2048, H.ITTS_BF16)
+    decode_path = "persistent" if kv.decode_path() == H.ITTS_DECODE_PERSISTENT else "multi-kernel"
+    print(f"[bench] decode step: {decode_path}", file=sys.stderr, flush=True)
     prompt = synth.make_prompt(cfg, n_cond, n_text, seed=args.seed + 1)
     sp = H.SamplingParams(max_mel_tokens=n_steps, **samp)
     cp = H.CodePrompt(prompt.text_tokens, prompt.conds, prompt.lang_id, None, n_steps)
@@ -192,7 +198,8 @@ def main():
         "data": "synthetic (seeded random-init weights of the reference architecture)",
         "config": {"workload": desc, "weights": f"int{bits} MLX-affine group 64, fp16 params",
                    "kv_cache": "bf16", "layers": 24, "d_model": 1280, "heads": 20,
-                   "prefill_rows": T, "decode_tokens": n_tok, "step": "one full generation"},
+                   "prefill_rows": T, "decode_tokens": n_tok, "step": "one full generation",
+                   "decode_path": decode_path},
         "ttft_ms": round(ttft_ms, 3),
         "decode_tokens_per_s": round(dec_steps / (dec_ms * 1e-3), 2),
         "decode_step_us": round(step_ms * 1e3, 2),

@@ -141,6 +141,18 @@ int32_t itts_gpt_max_cond(const itts_gpt *gpt);
 /* The HIP stream every kernel of this decoder runs on (hipStream_t). */
 void *itts_gpt_stream(const itts_gpt *gpt);
 
+/* Decode-step implementation (no counterpart in the reference, whose step is one MLX
+ * graph per token, gpt.rs:702-754).  AUTO: the persistent single-launch step wherever it
+ * supports the shape (8-bit codes, bf16 cache, one block per compute unit), else the
+ * multi-kernel step.  MULTI forces the multi-kernel step; PERSISTENT makes caches that
+ * cannot use it fail at creation.  Applies to caches created afterwards. */
+typedef enum itts_decode_path {
+  ITTS_DECODE_AUTO = 0,
+  ITTS_DECODE_MULTI = 1,
+  ITTS_DECODE_PERSISTENT = 2
+} itts_decode_path;
+itts_status itts_gpt_set_decode_path(itts_gpt *gpt, itts_decode_path path);
+
 /* ---- KvCache (gpt.rs:76-217) ---- */
 /* KvCache::new(max_seq); kv_dtype ITTS_BF16 (workload default) or ITTS_F32 (the
  * reference's storage type).  Capacity is preallocated; no growth copies. */
@@ -151,6 +163,8 @@ int32_t itts_kv_valid_len(const itts_kv *kv);          /* KvCache::valid_len */
 int32_t itts_kv_max_seq(const itts_kv *kv);            /* KvCache::max_seq */
 /* Copies layer `layer`'s K (which_v=0) or V (1) rows [n_head][valid_len][64] as fp32. */
 itts_status itts_kv_read(const itts_kv *kv, int32_t layer, int32_t which_v, float *out);
+/* The decode path this cache's steps take: ITTS_DECODE_MULTI or ITTS_DECODE_PERSISTENT. */
+itts_decode_path itts_kv_decode_path(const itts_kv *kv);
 
 /* ---- decoding (gpt.rs:636-754) ---- */
 /* Gpt::prefill: logits_out receives [mel_vocab] fp32 (may be NULL). */

@@ -48,6 +48,10 @@ struct DecodeCtl {
   int32_t last_tok;   // last sampled token (STOP included)
   uint64_t rng;       // SamplerRng state
   uint64_t seen[kSeenWords];
+  // Owned by the device: steps taken by the persistent decode kernel (the epoch base of
+  // its exchange words).  Host writes of the control block stop before this field.
+  int32_t xstep;
+  int32_t pad_;
 };
 
 // Sampling parameters as the device sampler consumes them.
@@ -163,6 +167,24 @@ __device__ inline void layernorm_to_lds(const float *x, const float *w, const fl
   const float var = block_sum<NT>(q, red) / (float)n;
   const float rstd = 1.0f / sqrtf(var + 1e-5f);
   for (int i = threadIdx.x; i < n; i += NT) xl[i] = (xl[i] - mean) * rstd * w[i] + b[i];
+  __syncthreads();
+}
+
+// LayerNorm of an LDS row x into the LDS row y.
+template <int NT>
+__device__ inline void layernorm_lds_inplace_to(const float *x, float *y, const float *w, const float *b, int n,
+                                                float *red) {
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) s += x[i];
+  const float mean = block_sum<NT>(s, red) / (float)n;
+  float q = 0.0f;
+  for (int i = threadIdx.x; i < n; i += NT) {
+    const float d = x[i] - mean;
+    q += d * d;
+  }
+  const float var = block_sum<NT>(q, red) / (float)n;
+  const float rstd = 1.0f / sqrtf(var + 1e-5f);
+  for (int i = threadIdx.x; i < n; i += NT) y[i] = (x[i] - mean) * rstd * w[i] + b[i];
   __syncthreads();
 }
 

@@ -90,12 +90,44 @@ hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt,
 
 hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipStream_t s);
 
-// Device sampler (one block).  mode 0: API call on `logits` (penalised in place,
-// token to *tok_out, rng advanced); mode 1: generate step driven by ctl.
+// Persistent decode step (kernels_persist.hip): one cooperative launch of B blocks
+// (one per CU) runs a whole decode step.  Exchange words are (epoch << 32 | fp32 bits).
+constexpr int kCntStride = 32;  // one 128-byte line per head counter
+// Every exchange array is followed by this many readable words: pollers read whole
+// batches without clamping.
+constexpr int kPersistPad = 2560;
+struct PersistArgs {
+  const DevLayer *layers;  // device array [n_layer]
+  int n_layer, d, H, F, V, S, B;
+  DevQL head;
+  const float *ln_f_w, *ln_f_b, *fn_w, *fn_b;
+  const float *mel_emb, *mel_pos;
+  void *kc, *vc;           // bf16 cache bases [n_layer][H][max_seq][64]
+  int max_seq;
+  DecodeCtl *ctl;
+  uint64_t *x_x, *x_qkv, *x_part, *x_attn, *x_mid, *x_f;  // [d] [3d] [H*S*66] [d] [d] [F]
+  uint32_t *cnt;           // [H * kCntStride] split counters (wrap at S; start at 0)
+  uint32_t *err;           // nonzero after a timed-out wait
+  float *logits;           // [V]
+  uint32_t ep_stride;      // epochs per step: 8 * (n_layer + 1)
+  int xin_len, part_len, own_len;  // LDS sizes (floats)
+};
+// Whether the persistent step supports this shape on B blocks; *S = attention splits.
+bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int *S);
+constexpr size_t kPersistMaxLds = 150 * 1024;
+size_t persist_lds_bytes(const PersistArgs &a);
+// Blocks of the persistent kernel that fit on one compute unit with `lds` bytes of LDS.
+hipError_t persist_blocks_per_cu(int ptype, size_t lds, int *blocks);
+hipError_t launch_decode_persist(PersistArgs a, int ptype, hipStream_t s);
+// Raises the kernel's dynamic-LDS limit; once per process, outside stream capture.
+hipError_t persist_init();
+
 // Raises the sampler's dynamic-LDS limit; call once per process before any launch
 // (never during stream capture).
 hipError_t sampler_init();
 
+// Device sampler (one block).  mode 0: API call on `logits` (penalised in place,
+// token to *tok_out, rng advanced); mode 1: generate step driven by ctl.
 hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSampling p,
                           uint64_t *rng, int32_t *tok_out, DecodeCtl *ctl, int32_t *codes,
                           int stop_tok, int mode, hipStream_t s);

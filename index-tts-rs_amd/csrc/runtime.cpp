@@ -116,6 +116,11 @@ struct itts_gpt {
   std::vector<DevLayer> layers;
   DevBuf ln_f_w, ln_f_b, fn_w, fn_b;
   DevQL head{};
+  // persistent decode step: device copy of `layers`, blocks (one per compute unit)
+  DevBuf dlayers;
+  int n_cu = 0;
+  bool persist_ok = false;  // kernels set up and 8-bit codes
+  itts_decode_path path = ITTS_DECODE_AUTO;
   // decode workspace
   DevBuf x, q, a, f, logits;
   // prefill workspace (grown on demand)
@@ -136,6 +141,10 @@ struct itts_kv {
   DevBuf codes;        // generate output
   DecodeCtl *host_ctl = nullptr;  // pinned staging, 2 slots
   int splits = 0;
+  // persistent decode step: exchange words, split counters + error word, arguments
+  bool persist = false;
+  DevBuf xch, sync;
+  PersistArgs pa{};
   // captured decode iteration (sampler + step), keyed by the sampling parameters
   hipGraphExec_t gexec = nullptr;
   hipGraph_t graph = nullptr;
@@ -272,6 +281,10 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
 // Enqueues one decode step driven by kv->ctl (token, position and cache length read on
 // the device): logits land in gpt->logits and ctl->valid_len advances.
 itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
+  if (kv->persist) {
+    HIP_TRY(launch_decode_persist(kv->pa, g->ptype(), g->stream));
+    return ITTS_OK;
+  }
   const itts_config &c = g->cfg;
   const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
@@ -399,11 +412,101 @@ itts_status run_prefill(itts_gpt *g, itts_kv *kv, const int32_t *text, int32_t n
   return ITTS_OK;
 }
 
-// Writes the host-known fields of the decode control block.
+// Writes the host-known fields of the decode control block (the device-owned step
+// counter that follows them is left alone).
 itts_status write_ctl(itts_kv *kv, const DecodeCtl &h) {
   *kv->host_ctl = h;
-  HIP_TRY(hipMemcpyAsync(kv->ctl.p, kv->host_ctl, sizeof(DecodeCtl), hipMemcpyHostToDevice,
+  HIP_TRY(hipMemcpyAsync(kv->ctl.p, kv->host_ctl, offsetof(DecodeCtl, xstep), hipMemcpyHostToDevice,
                          kv->gpt->stream));
+  return ITTS_OK;
+}
+
+// After the stream has drained: a persistent step whose exchange wait timed out leaves
+// the error word set and its step unfinished.  The exchange state is cleared so that the
+// cache stays usable, and the call reports a device error.
+itts_status check_persist(itts_kv *kv) {
+  if (!kv->persist) return ITTS_OK;
+  hipStream_t s = kv->gpt->stream;
+  uint32_t err = 0;
+  HIP_TRY(hipMemcpyAsync(&err, kv->pa.err, sizeof err, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (err == 0) return ITTS_OK;
+  HIP_TRY(hipMemsetAsync(kv->xch.p, 0, kv->xch.bytes, s));
+  HIP_TRY(hipMemsetAsync(kv->sync.p, 0, kv->sync.bytes, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return set_error(ITTS_E_DEVICE, "decode step: a persistent-kernel exchange wait timed out");
+}
+
+// Sets up the persistent decode step for a new cache when the decoder and the cache
+// shape allow it.  *used reports whether the cache takes that path.
+itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
+  *used = false;
+  const itts_config &c = g->cfg;
+  int S = 0;
+  const bool shape_ok = g->persist_ok && kv->kvt == kKvBf16 &&
+                        persist_supported(c.d_model, c.d_ffn, c.mel_vocab, c.n_head, c.n_layer, kv->max_seq,
+                                          g->n_cu, &S);
+  PersistArgs a{};
+  const int d = c.d_model, F = c.d_ffn, H = c.n_head, V = c.mel_vocab, B = g->n_cu;
+  if (shape_ok) {
+    a.n_layer = c.n_layer;
+    a.d = d;
+    a.H = H;
+    a.F = F;
+    a.V = V;
+    a.S = S;
+    a.B = B;
+    a.xin_len = std::max(d, F);
+    auto cap = [&](int N, int C) { return ((N + B - 1) / B) * C; };
+    a.part_len = std::max({cap(3 * d, d / 16), cap(d, d / 16), cap(F, d / 16), cap(d, F / 16), cap(V, d / 16)});
+    a.own_len = (d + B - 1) / B;
+  }
+  bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
+  if (ok) {
+    int per_cu = 0;
+    HIP_TRY(persist_blocks_per_cu(g->ptype(), persist_lds_bytes(a), &per_cu));
+    ok = per_cu >= 1;  // one block per compute unit, all co-resident
+  }
+  if (g->path == ITTS_DECODE_PERSISTENT && !ok)
+    return set_error(ITTS_E_VALIDATION,
+                     "decode_path: the persistent decode step does not support this cache (bf16 rows, "
+                     "max_seq %d, %d compute units)",
+                     kv->max_seq, B);
+  if (!ok || g->path == ITTS_DECODE_MULTI) return ITTS_OK;
+  // exchange arrays, each followed by kPersistPad readable words
+  const size_t P = kPersistPad;
+  const size_t n_x = d + P, n_qkv = 3 * (size_t)d + P, n_part = (size_t)H * S * 66 + P, n_f = F + P;
+  const size_t words = n_x + n_qkv + n_part + n_x + n_x + n_f;
+  const size_t sync_words = (size_t)H * kCntStride + 64;
+  HIP_TRY(kv->xch.ensure(words * sizeof(uint64_t)));
+  HIP_TRY(kv->sync.ensure(sync_words * sizeof(uint32_t)));
+  HIP_TRY(hipMemsetAsync(kv->xch.p, 0, kv->xch.bytes, g->stream));
+  HIP_TRY(hipMemsetAsync(kv->sync.p, 0, kv->sync.bytes, g->stream));
+  uint64_t *x = kv->xch.as<uint64_t>();
+  a.x_x = x;
+  a.x_qkv = a.x_x + n_x;
+  a.x_part = a.x_qkv + n_qkv;
+  a.x_attn = a.x_part + n_part;
+  a.x_mid = a.x_attn + n_x;
+  a.x_f = a.x_mid + n_x;
+  a.cnt = kv->sync.as<uint32_t>();
+  a.err = a.cnt + (size_t)H * kCntStride;
+  a.layers = g->dlayers.as<DevLayer>();
+  a.head = g->head;
+  a.ln_f_w = g->ln_f_w.as<float>();
+  a.ln_f_b = g->ln_f_b.as<float>();
+  a.fn_w = g->fn_w.as<float>();
+  a.fn_b = g->fn_b.as<float>();
+  a.mel_emb = g->mel_emb.as<float>();
+  a.mel_pos = g->mel_pos.as<float>();
+  a.kc = kv->k.p;
+  a.vc = kv->v.p;
+  a.max_seq = kv->max_seq;
+  a.ctl = kv->ctl.as<DecodeCtl>();
+  a.logits = g->logits.as<float>();
+  a.ep_stride = 8u * (uint32_t)(c.n_layer + 1);
+  kv->pa = a;
+  *used = true;
   return ITTS_OK;
 }
 
@@ -536,6 +639,16 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
   QLHost &hq = g->qls[(size_t)c.n_layer * 4];
   if (itts_status st = upload_ql(hq, w->mel_head, c.mel_vocab, d, bits, f32, "mel_head")) return fail(st);
   g->head = hq.dev();
+  if (upload(g->dlayers, g->layers.data(), sizeof(DevLayer) * c.n_layer) != hipSuccess)
+    return fail(set_error(ITTS_E_DEVICE, "upload of the layer table failed"));
+  {
+    int dev = 0, coop = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&g->n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
+      return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
+    g->persist_ok = bits == 8 && coop != 0 && persist_init() == hipSuccess;
+  }
   if (g->x.ensure(sizeof(float) * d) || g->q.ensure(sizeof(float) * d) || g->a.ensure(sizeof(float) * d) ||
       g->f.ensure(sizeof(float) * F) || g->logits.ensure(sizeof(float) * c.mel_vocab))
     return fail(set_error(ITTS_E_DEVICE, "workspace allocation failed"));
@@ -562,6 +675,17 @@ int32_t itts_gpt_num_layers(const itts_gpt *gpt) { return gpt ? gpt->cfg.n_layer
 int32_t itts_gpt_max_cond(const itts_gpt *gpt) { return gpt ? gpt->max_cond : 0; }
 void *itts_gpt_stream(const itts_gpt *gpt) { return gpt ? (void *)gpt->stream : nullptr; }
 
+itts_status itts_gpt_set_decode_path(itts_gpt *gpt, itts_decode_path path) {
+  if (!gpt) return set_error(ITTS_E_VALIDATION, "decode_path: null decoder");
+  if (path != ITTS_DECODE_AUTO && path != ITTS_DECODE_MULTI && path != ITTS_DECODE_PERSISTENT)
+    return set_error(ITTS_E_VALIDATION, "decode_path: unknown path %d", (int)path);
+  if (path == ITTS_DECODE_PERSISTENT && !gpt->persist_ok)
+    return set_error(ITTS_E_VALIDATION,
+                     "decode_path: the persistent decode step needs 8-bit codes and cooperative launch");
+  gpt->path = path;
+  return ITTS_OK;
+}
+
 itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, itts_kv **out) {
   if (!gpt || !out) return set_error(ITTS_E_VALIDATION, "kv_cache: null argument");
   if (max_seq <= 0) return set_error(ITTS_E_VALIDATION, "max_seq: KV cache max_seq must be >= 1");
@@ -583,7 +707,16 @@ itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, 
   }
   if (hipMemsetAsync(kv->k.p, 0, n * es, gpt->stream) != hipSuccess ||
       hipMemsetAsync(kv->v.p, 0, n * es, gpt->stream) != hipSuccess ||
-      hipStreamSynchronize(gpt->stream) != hipSuccess) {
+      hipMemsetAsync(kv->ctl.p, 0, sizeof(DecodeCtl), gpt->stream) != hipSuccess) {
+    delete kv;
+    return set_error(ITTS_E_DEVICE, "KV cache initialisation failed");
+  }
+  if (itts_status st = setup_persist(gpt, kv, &kv->persist)) {
+    (void)hipStreamSynchronize(gpt->stream);
+    delete kv;
+    return st;
+  }
+  if (hipStreamSynchronize(gpt->stream) != hipSuccess) {
     delete kv;
     return set_error(ITTS_E_DEVICE, "KV cache initialisation failed");
   }
@@ -605,6 +738,9 @@ void itts_kv_reset(itts_kv *kv) {
 }
 int32_t itts_kv_valid_len(const itts_kv *kv) { return kv ? kv->valid_len : 0; }
 int32_t itts_kv_max_seq(const itts_kv *kv) { return kv ? kv->max_seq : 0; }
+itts_decode_path itts_kv_decode_path(const itts_kv *kv) {
+  return kv && kv->persist ? ITTS_DECODE_PERSISTENT : ITTS_DECODE_MULTI;
+}
 
 itts_status itts_kv_read(const itts_kv *kv, int32_t layer, int32_t which_v, float *out) {
   if (!kv || !out) return set_error(ITTS_E_VALIDATION, "kv_cache: null argument");
@@ -674,6 +810,7 @@ itts_status itts_gpt_step(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int3
     HIP_TRY(hipMemcpyAsync(logits_out, gpt->logits.p, sizeof(float) * c.mel_vocab, hipMemcpyDeviceToHost,
                            gpt->stream));
   HIP_TRY(hipStreamSynchronize(gpt->stream));
+  if (itts_status st = check_persist(kv)) return st;
   kv->valid_len += 1;
   return ITTS_OK;
 }
@@ -785,7 +922,9 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     return enqueue_decode_step(gpt, kv);
   };
   // capture one decode iteration (sample, then step) once per cache and parameters
-  if (gpt->use_graph && (!kv->have_graph || !same_sampling(kv->gkey, ds))) {
+  // the persistent step is a cooperative launch: enqueued directly, never captured
+  const bool use_graph = gpt->use_graph && !kv->persist;
+  if (use_graph && (!kv->have_graph || !same_sampling(kv->gkey, ds))) {
     if (kv->gexec) {
       (void)hipGraphExecDestroy(kv->gexec);
       kv->gexec = nullptr;
@@ -826,7 +965,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   };
   auto launch_batch = [&](int which) -> hipError_t {
     for (int i = 0; i < batch; i++) {
-      if (gpt->use_graph) {
+      if (use_graph) {
         hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
         if (e != hipSuccess) return e;
       } else if (enqueue_iteration() != ITTS_OK) {
@@ -858,6 +997,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   if (e == hipSuccess) e = hipStreamSynchronize(gpt->stream);
   cleanup();
   HIP_TRY(e);
+  if (itts_status pst = check_persist(kv)) return pst;
   DecodeCtl fin{};
   HIP_TRY(hipMemcpy(&fin, kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost));
   if (!fin.done) return set_error(ITTS_E_INTERNAL, "generation did not reach its end");

@@ -30,6 +30,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libitts_hip.so")
 
 ITTS_OK, ITTS_E_VALIDATION, ITTS_E_WEIGHT, ITTS_E_DEVICE, ITTS_E_CAPACITY, ITTS_E_INTERNAL = range(6)
 ITTS_F16, ITTS_F32, ITTS_BF16 = 1, 2, 3
+ITTS_DECODE_AUTO, ITTS_DECODE_MULTI, ITTS_DECODE_PERSISTENT = 0, 1, 2
 
 GPT_MEL_VOCAB = 8194
 START_TEXT_TOKEN, STOP_TEXT_TOKEN = 0, 1
@@ -118,12 +119,14 @@ _SIGS = {
     "itts_gpt_num_layers": (C.c_int32, [C.c_void_p]),
     "itts_gpt_max_cond": (C.c_int32, [C.c_void_p]),
     "itts_gpt_stream": (C.c_void_p, [C.c_void_p]),
+    "itts_gpt_set_decode_path": (C.c_int, [C.c_void_p, C.c_int]),
     "itts_kv_create": (C.c_int, [C.c_void_p, C.c_int32, C.c_int, C.POINTER(C.c_void_p)]),
     "itts_kv_destroy": (None, [C.c_void_p]),
     "itts_kv_reset": (None, [C.c_void_p]),
     "itts_kv_valid_len": (C.c_int32, [C.c_void_p]),
     "itts_kv_max_seq": (C.c_int32, [C.c_void_p]),
     "itts_kv_read": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
+    "itts_kv_decode_path": (C.c_int, [C.c_void_p]),
     "itts_gpt_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
                                    C.c_int32, C.c_int32, C.c_void_p]),
     "itts_gpt_prefill_after": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
@@ -277,6 +280,10 @@ class Gpt:
     def stream(self) -> int:
         return lib.itts_gpt_stream(self._h)
 
+    def set_decode_path(self, path: int):
+        """ITTS_DECODE_AUTO / _MULTI / _PERSISTENT for caches created afterwards."""
+        _check(lib.itts_gpt_set_decode_path(self._h, int(path)))
+
     def kv_cache(self, max_seq: int = 2048, dtype: int = ITTS_BF16) -> "KvCache":
         return KvCache(self, max_seq, dtype)
 
@@ -342,6 +349,9 @@ class KvCache:
 
     def max_seq(self) -> int:
         return lib.itts_kv_max_seq(self._h)
+
+    def decode_path(self) -> int:
+        return lib.itts_kv_decode_path(self._h)
 
     def last_timing(self) -> dict:
         t = itts_timing()

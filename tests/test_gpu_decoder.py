@@ -25,13 +25,25 @@ def say(*a):
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module")
-def model():
-    say("[gpu] tiny decoder: weights + upload")
+# "persistent" runs AUTO, which picks the persistent step for every bf16 cache here (and
+# the multi-kernel step for fp32 caches); "multi" forces the multi-kernel step.
+PATHS = {"persistent": H.ITTS_DECODE_AUTO, "multi": H.ITTS_DECODE_MULTI}
+
+
+@pytest.fixture(scope="module", params=["persistent", "multi"])
+def model(request):
+    say(f"[gpu] tiny decoder ({request.param} decode step): weights + upload")
     W = synth.make_weights(synth.TINY_CONFIG, seed=21, init="rich")
     g = H.Gpt(W)
+    g.set_decode_path(PATHS[request.param])
+    g.path = H.ITTS_DECODE_PERSISTENT if request.param == "persistent" else H.ITTS_DECODE_MULTI
     yield W, g, ito.Model(W)
     g.close()
+
+
+def expect_path(g, kv, kvt=H.ITTS_BF16):
+    want = g.path if kvt == H.ITTS_BF16 else H.ITTS_DECODE_MULTI
+    assert kv.decode_path() == want
 
 
 @pytest.mark.parametrize("kvt", [H.ITTS_BF16, H.ITTS_F32])
@@ -40,6 +52,7 @@ def test_prefill_and_steps_match_oracle(model, kvt):
     say(f"[gpu] prefill+steps kv={kvt}")
     pr = synth.make_prompt(W.cfg, 3, 20, seed=1)
     kv = g.kv_cache(256, kvt)
+    expect_path(g, kv, kvt)
     okv = M.kv(256, kv_bf16=kvt == H.ITTS_BF16)
     a = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
     b = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)
@@ -81,6 +94,7 @@ def test_generate_tokens_identical_to_oracle(model, greedy):
                          repetition_penalty=10.0, max_mel_tokens=150)
     seed = 20240607
     kv = g.kv_cache(512)
+    expect_path(g, kv)
     rng = H.SamplerRng(seed)
     codes = H.generate_codes_after(g, H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, 150),
                                    kv, p, rng)
@@ -99,6 +113,8 @@ def test_generate_stops_and_respects_min_codes(model):
     W2 = copy.deepcopy(W)
     W2.head.bias[W.cfg["mel_vocab"] - 1] = 100.0
     g2 = H.Gpt(W2)
+    g2.set_decode_path(H.ITTS_DECODE_AUTO if model[1].path == H.ITTS_DECODE_PERSISTENT
+                       else H.ITTS_DECODE_MULTI)
     pr = synth.make_prompt(W.cfg, 3, 8, seed=4)
     p = H.SamplingParams(greedy=True, max_mel_tokens=40)
     kv = g2.kv_cache(256)
@@ -164,3 +180,17 @@ def test_validation_and_capacity_errors(model):
     with pytest.raises(H.CapacityError):
         g.step(kv, 5, 40)
     assert kv.valid_len() == 32
+
+
+def test_forced_persistent_rejects_fp32_cache(model):
+    W, g, _ = model
+    if g.path != H.ITTS_DECODE_PERSISTENT:
+        pytest.skip("persistent-path case")
+    g.set_decode_path(H.ITTS_DECODE_PERSISTENT)
+    try:
+        with pytest.raises(H.ValidationError) as e:
+            g.kv_cache(64, H.ITTS_F32)
+        assert e.value.message.startswith("decode_path")
+        assert g.kv_cache(64).decode_path() == H.ITTS_DECODE_PERSISTENT
+    finally:
+        g.set_decode_path(H.ITTS_DECODE_AUTO)
