@@ -93,9 +93,9 @@ hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipS
 // Persistent decode step (kernels_persist.hip): one cooperative launch of B blocks
 // (one per CU) runs a whole decode step.  Exchange words are (epoch << 32 | fp32 bits).
 constexpr int kCntStride = 32;  // one 128-byte line per head counter
-// Every exchange array is followed by this many readable words: pollers read whole
-// batches without clamping.
-constexpr int kPersistPad = 2560;
+// Every exchange array is followed by this many readable words (a polling wave reads up
+// to 63 words past the end of what it needs).
+constexpr int kPersistPad = 64;
 struct PersistArgs {
   const DevLayer *layers;  // device array [n_layer]
   int n_layer, d, H, F, V, S, B;
@@ -110,7 +110,9 @@ struct PersistArgs {
   uint32_t *err;           // nonzero after a timed-out wait
   float *logits;           // [V]
   uint32_t ep_stride;      // epochs per step: 8 * (n_layer + 1)
-  int xin_len, part_len, own_len;  // LDS sizes (floats)
+  // LDS region sizes (floats, multiples of 4): input row, per-chunk partials, residual
+  // slice, row outputs, attention partials of one head, one layer's staged parameters
+  int xin_len, part_len, own_len, out_len, pp_len, lp_len;
 };
 // Whether the persistent step supports this shape on B blocks; *S = attention splits.
 bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int *S);

@@ -4,24 +4,35 @@
 // Why persistent.  A batch-1 step is a chain of ~120 dependent GEMV/attention phases over
 // small matrices.  As separate kernels each phase pays the launch floor (~2 us) plus the
 // loaded HBM latency (~1.7 us) before its first weight byte arrives.  Here every block
-// keeps its share of each phase's weights in registers and prefetches the next layer's
-// share as soon as the current one is consumed, so HBM latency overlaps the dependency
-// chain; what is left per phase is the exchange of the phase's output vector.
+// keeps its share of each matrix in registers, loaded two matrices ahead of use, so HBM
+// latency overlaps the dependency chain; what is left per phase is the exchange of the
+// phase's output vector between blocks.
 //
 // Exchange.  Every cross-block value travels as one 64-bit word (epoch << 32 | fp32 bits)
 // written and read with device-scope relaxed atomics: a reader polls the words it needs
 // until each carries the phase's epoch, so no fence or grid barrier is needed and a stale
 // word is never mistaken for a fresh one.  Epoch of (step s, layer l, phase p):
-// s * 8 * (n_layer + 1) + 8 * l + p + 1, with s from the control block.
+// s * 8 * (n_layer + 1) + 8 * l + p + 1, with s from the control block.  A word is
+// rewritten only after every block has consumed it: the next write of any array depends
+// on every block's output of a later phase.
 //
-// Waves.  Waves 0-1 ("pollers") poll exchange words into LDS; waves 2-7 ("compute") hold
-// the weights.  Vector loads complete in issue order per wave, so a wave with prefetches
-// in flight would not see a poll result before its prefetches land: the roles never mix.
-// All waves meet at __syncthreads, which on gfx950 waits for LDS traffic only.
+// Wave roles.  Vector memory operations of one wave complete in issue order (stores
+// included), and the compiler waits for them by count.  So that no wave ever waits for
+// an unrelated operation, each wave kind issues one kind of global access:
+//   pollers  (waves 0-5)  : loads only - exchange polls, the embedding;
+//   publisher (wave 6)    : exchange words, K/V cache rows and logits (stores), and the
+//                           next layer's parameters (loads it waits for, while no other
+//                           work depends on it);
+//   loaders  (waves 7-15) : loads only, all unconditional - the weight slices (two
+//                           matrices ahead) and the attention K/V rows; they compute
+//                           the dot products and row sums in LDS.
+// Every wave takes part in every __syncthreads, which on gfx950 waits for LDS traffic
+// only.  LayerNorm parameters and bias rows reach the loaders through LDS, staged one
+// layer ahead (double buffer).
 //
 // Ownership.  For a matrix with N rows, block b owns rows [N*b/B, N*(b+1)/B).  A block's
 // rows of c_proj and of the MLP's c_proj coincide, so it keeps its slice of the residual
-// stream locally.  Attention: block b < H*S serves head b/S over key split b%S; the last
+// stream in LDS.  Attention: block b < H*S serves head b/S over key split b%S; the last
 // split of a head to finish (device-scope counter) combines the head's partials.
 //
 // Every wait is bounded: a timed-out poller raises the error word, and every block leaves
@@ -34,21 +45,24 @@ namespace itts {
 
 namespace {
 
-// 512 threads: with two waves per SIMD each wave may hold 256 registers, room for two
-// matrices' weight slices plus a poll batch.
-constexpr int kThreads = 512;
-constexpr int kPollThreads = 128;     // waves 0-1
-constexpr int kComputeThreads = 384;  // waves 2-7
-constexpr int kComputeWaves = kComputeThreads / 64;
-constexpr int kKeySlots = kComputeThreads / 8;  // attention: 8 lanes per key
-constexpr int kKeyPasses = 4;                   // keys per split <= kKeySlots * kKeyPasses
-constexpr int kPollBatch = 20;        // exchange words per poller thread in flight
-constexpr int kPollSpan = kPollThreads * kPollBatch;
-static_assert(kPollSpan <= kPersistPad, "exchange padding must cover one poll batch");
+constexpr int kThreads = 1024;
+constexpr int kPollWaves = 6;
+constexpr int kPollThreads = kPollWaves * 64;  // waves 0-5
+constexpr int kPubWave = 6;
+constexpr int kLoadWave0 = 7;
+constexpr int kLoadWaves = 9;
+constexpr int kLoadThreads = kLoadWaves * 64;  // waves 7-15
+constexpr int kKeySlots = kLoadThreads / 8;    // attention: 8 lanes per key
+constexpr int kKeyPasses = 3;                  // keys per split <= kKeySlots * kKeyPasses
+// exchange words per poller lane in flight: one batch covers a d_model vector (1280) or
+// the MLP vector (5120) of the full-size decoder
+constexpr int kPollD = 4, kPollF = 14;
 constexpr long kSpinLimit = 1L << 21;
-// 16-byte code chunks per compute lane (rows per block x chunks per row / 384, rounded
-// up) for the full-size decoder on 256 blocks
-constexpr int kSlQkv = 4, kSlProj = 2, kSlFc = 5, kSlMp = 5, kSlHead = 7;
+static_assert(kPollThreads % 64 == 0, "pollers are whole waves");
+static_assert(kPersistPad >= 64, "a polling wave may read up to 63 words past n");
+// 16-byte code chunks per loader lane (rows per block x chunks per row / 576, rounded up)
+// for the full-size decoder on 256 blocks
+constexpr int kSlQkv = 3, kSlProj = 1, kSlFc = 3, kSlMp = 3, kSlHead = 5;
 
 struct RowMap {
   int row0, rows, C;  // first row, row count, 16-byte chunks per row
@@ -69,26 +83,66 @@ __device__ inline uint32_t ld_u32(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Pollers: read n exchange words of epoch ep into dst (LDS).  False on timeout or when
-// another block raised the error word.  src must stay readable for kPollSpan words past
-// n: the exchange arrays carry that much padding, so the loads need no clamping.
-__device__ bool poll_words(const uint64_t *src, int n, uint32_t ep, float *dst, uint32_t *err) {
-  const int t = threadIdx.x;
-  for (int base = 0; base < n; base += kPollSpan) {
-    const int lim = n - base - t;  // word k of this lane is in range when 128k < lim
-    uint64_t w[kPollBatch];
+// Cross-lane reductions with DPP (ALU row shifts and broadcasts, no LDS round trip).  They
+// need every lane of the wave active.  Fixed order, so every block reduces identically.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ inline float dpp_f(float v, float old) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+// Inclusive scan within each row of 16 lanes: lane 15 of a row holds the row's sum.
+__device__ inline float row16_sum(float x) {
+  x += dpp_f<0x111, 0xf, 0xf>(x, 0.0f);  // row_shr:1
+  x += dpp_f<0x112, 0xf, 0xf>(x, 0.0f);  // row_shr:2
+  x += dpp_f<0x114, 0xf, 0xe>(x, 0.0f);  // row_shr:4, lanes 4-15
+  x += dpp_f<0x118, 0xf, 0xc>(x, 0.0f);  // row_shr:8, lanes 8-15
+  return x;
+}
+// Sum over the wave, returned to every lane.
+__device__ inline float wave64_sum(float x) {
+  x = row16_sum(x);
+  x += dpp_f<0x142, 0xa, 0xf>(x, 0.0f);  // row_bcast:15 into rows 1, 3
+  x += dpp_f<0x143, 0xc, 0xf>(x, 0.0f);  // row_bcast:31 into rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+// Max over the wave, returned to every lane.
+__device__ inline float wave64_max(float x) {
+  const float ni = -INFINITY;
+  x = fmaxf(x, dpp_f<0x111, 0xf, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x112, 0xf, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x114, 0xf, 0xe>(x, ni));
+  x = fmaxf(x, dpp_f<0x118, 0xf, 0xc>(x, ni));
+  x = fmaxf(x, dpp_f<0x142, 0xa, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x143, 0xc, 0xf>(x, ni));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// Pollers: read n exchange words of epoch ep into dst (LDS).  A wave issues a batch load
+// only when its first lane's word is in range (a wave-uniform test), so lanes read at
+// most 63 words past n; the exchange arrays carry that padding.  False on timeout or
+// when another block raised the error word.
+template <int NB>
+__device__ __forceinline__ bool poll_words(const uint64_t *src, int n, uint32_t ep, float *dst, uint32_t *err, int t,
+                           float *xsum = nullptr) {
+  const int wb = t & ~63;
+  for (int base = 0; base < n; base += NB * kPollThreads) {
+    uint64_t w[NB];
     long spins = 0;
     while (true) {
-      // lane offset made opaque per spin: the compiler keeps one base register instead of
-      // hoisting a 64-bit address per word (per call site) out of the loops
+      // lane offset made opaque per spin: one base register instead of a hoisted 64-bit
+      // address per word and call site
       uint32_t to = (uint32_t)(base + t) * 8u;
       asm volatile("" : "+v"(to));
       const uint64_t *p = reinterpret_cast<const uint64_t *>(reinterpret_cast<const char *>(src) + to);
 #pragma unroll
-      for (int k = 0; k < kPollBatch; k++) w[k] = ll_load(p + k * kPollThreads);
+      for (int k = 0; k < NB; k++) {
+        w[k] = 0;
+        if (base + wb + k * kPollThreads < n) w[k] = ll_load(p + k * kPollThreads);
+      }
       bool all = true;
 #pragma unroll
-      for (int k = 0; k < kPollBatch; k++) all = all && (kPollThreads * k >= lim || (uint32_t)(w[k] >> 32) == ep);
+      for (int k = 0; k < NB; k++)
+        all = all && (base + t + k * kPollThreads >= n || (uint32_t)(w[k] >> 32) == ep);
       if (__all(all)) break;
       if (++spins > kSpinLimit) {
         __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -98,16 +152,37 @@ __device__ bool poll_words(const uint64_t *src, int n, uint32_t ep, float *dst, 
       __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
-    for (int k = 0; k < kPollBatch; k++)
-      if (kPollThreads * k < lim) dst[base + t + kPollThreads * k] = __uint_as_float((uint32_t)w[k]);
+    for (int k = 0; k < NB; k++) {
+      const int i = base + t + kPollThreads * k;
+      const float v = i < n ? __uint_as_float((uint32_t)w[k]) : 0.0f;
+      if (i < n) dst[i] = v;
+      if (xsum) {
+        // 16 consecutive lanes hold 16 consecutive words (kPollThreads is a multiple of
+        // 16): their sum is the chunk sum the GEMV consumes
+        const float c = row16_sum(v);
+        if ((t & 15) == 15 && i < n) xsum[i >> 4] = c;
+      }
+    }
   }
   return true;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Load through the global address space.  Pointers read from the layer table are generic
+// to the compiler, and a generic (flat) load also counts against the LDS wait counter, so
+// every LDS wait of a wave would wait for its weight prefetches too.
+template <class T>
+__device__ inline T gld(const void *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
 }
 
 // (scale, bias) of one group as held in registers: fp16x2 in one register, or float2.
 template <int PT>
 struct ParamReg {
-  using type = float2;
+  using type = f32x2;
 };
 template <>
 struct ParamReg<kParamF16> {
@@ -116,37 +191,37 @@ struct ParamReg<kParamF16> {
 __device__ inline float2 param_value(uint32_t w) {
   return make_float2(half_bits_to_float(w & 0xffffu), half_bits_to_float(w >> 16));
 }
-__device__ inline float2 param_value(float2 p) { return p; }
+__device__ inline float2 param_value(f32x2 p) { return make_float2(p.x, p.y); }
 
 template <int PT, int NS>
 struct Slots {
-  uint4 c[NS];
+  u32x4 c[NS];
   typename ParamReg<PT>::type p[NS];
 };
 
-// Compute lane cl (0..383) loads its chunks of the block's rows of ql (int8 codes).
-// The rows are contiguous and a row is C = K/16 chunks, so chunk c of the block sits at
-// codes + row0*K + 16c and its group parameters at params[row0*K/64 + c/4].
+// Loader lane ll (0..575) loads its chunks of the block's rows of ql (int8 codes).  The
+// rows are contiguous and a row is C = K/16 chunks, so chunk c of the block sits at
+// codes + row0*K + 16c with its group parameters at params[row0*K/64 + c/4].  Every load
+// is issued (a chunk past the block's share reads chunk 0 instead, row row0 < N always
+// exists), so the number of loads in flight is the same on every path.
 template <int PT, int NS>
-__device__ inline void load_slots(Slots<PT, NS> &s, const DevQL &ql, const RowMap &m, int cl) {
+__device__ inline void load_slots(Slots<PT, NS> &s, const DevQL &ql, const RowMap &m, int ll) {
   using P = typename ParamReg<PT>::type;
   const int total = m.rows * m.C;
   const char *cb = reinterpret_cast<const char *>(ql.codes + (size_t)m.row0 * ql.K);
   const char *pb = reinterpret_cast<const char *>(static_cast<const P *>(ql.params) + (size_t)m.row0 * (ql.K / kGroup));
-  // uniform base + 32-bit lane offset (a block's slice is far below 4 GiB)
-  uint32_t lo = (uint32_t)cl;
+  uint32_t lo = (uint32_t)ll;
   asm volatile("" : "+v"(lo));
 #pragma unroll
   for (int j = 0; j < NS; j++) {
-    const uint32_t c = lo + (uint32_t)(kComputeThreads * j);
-    if ((int)c < total) {
-      s.c[j] = *reinterpret_cast<const uint4 *>(cb + c * 16u);
-      s.p[j] = *reinterpret_cast<const P *>(pb + (c >> 2) * (uint32_t)sizeof(P));
-    }
+    uint32_t c = lo + (uint32_t)(kLoadThreads * j);
+    c = (int)c < total ? c : 0u;
+    s.c[j] = gld<u32x4>(cb + c * 16u);
+    s.p[j] = gld<P>(pb + (c >> 2) * (uint32_t)sizeof(P));
   }
 }
 
-__device__ inline float dot16(const uint4 c, const float *xc) {
+__device__ inline float dot16(const u32x4 c, const float *xc) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
   float acc = 0.0f;
 #pragma unroll
@@ -160,14 +235,18 @@ __device__ inline float dot16(const uint4 c, const float *xc) {
   return acc;
 }
 
-// Compute lanes: per-chunk partial products into part[] (LDS).
+// Loaders: per-chunk partial products into part[] (LDS).
 template <int PT, int NS>
 __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const float *xn, const float *xsum,
-                                 float *part, int cl) {
+                                 float *part, int ll) {
   const int total = m.rows * m.C;
+  // per-slot chunk indices are recomputed per call rather than hoisted out of the layer
+  // loop (they would hold a register per slot and matrix for the whole step)
+  uint32_t lo = (uint32_t)ll;
+  asm volatile("" : "+v"(lo));
 #pragma unroll
   for (int j = 0; j < NS; j++) {
-    const int c = cl + kComputeThreads * j;
+    const int c = (int)lo + kLoadThreads * j;
     if (c < total) {
       const int kc = c % m.C;
       const float2 p = param_value(s.p[j]);
@@ -178,115 +257,196 @@ __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const 
   }
 }
 
-// Compute wave cw sums rows cw, cw+6, ... of part[] in a fixed order; lane 0 receives
-// the row value with its bias and calls epi(row_in_block, value).
+// Loader waves sum the rows of part[] (a row is m.C chunk partials): 16 lanes per row,
+// four rows per wave, rows lw*4.. of each pass of 9 waves; in a fixed order.  The last
+// lane of a row receives the row value plus its bias (LDS) and calls epi(row, value).
 template <class Epi>
-__device__ inline void row_sums(const RowMap &m, const float *part, const float *bias, int cw, int lane, Epi epi) {
-  for (int r = cw; r < m.rows; r += kComputeWaves) {
+__device__ inline void row_sums(const RowMap &m, const float *part, const float *bias, int lw, int lane, Epi epi) {
+  const int sub = lane >> 4, sl = lane & 15;
+  for (int r0 = lw * 4; r0 < m.rows; r0 += kLoadWaves * 4) {
+    const int r = r0 + sub;
     float acc = 0.0f;
-    for (int c = lane; c < m.C; c += 64) acc += part[r * m.C + c];
-    acc = wave_sum(acc);
-    if (lane == 0) epi(r, acc + bias[m.row0 + r]);
+    if (r < m.rows)
+      for (int c = sl; c < m.C; c += 16) acc += part[r * m.C + c];
+    acc = row16_sum(acc);
+    if (sl == 15 && r < m.rows) epi(r, acc + bias[r]);
   }
 }
 
-__device__ inline void chunk_sums(const float *x, int n, float *xsum) {
-  for (int c = threadIdx.x; c < n / 16; c += kThreads) {
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) s += x[c * 16 + i];
-    xsum[c] = s;
+// Stages the LayerNorm parameters (4 x d) and the block's bias rows of layer l (or, for
+// l == n_layer, of the head) into one parameter buffer with LDS-DMA copies issued by one
+// wave (lane in [0, 64)): no registers are written, and nothing waits for the copies until
+// the wave's own s_waitcnt, placed where the wave has slack.  d is a multiple of 64.
+__device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, float *lp, const RowMap &mq,
+                                                 const RowMap &mp, const RowMap &mf, const RowMap &mm,
+                                                 const RowMap &mh, int lane) {
+  typedef __attribute__((address_space(3))) void *lds_ptr;
+  const int d = a.d;
+  const bool head = l >= a.n_layer;
+  const DevLayer *Ly = head ? nullptr : a.layers + l;
+  const float *v0 = head ? a.ln_f_w : Ly->ln1_w, *v1 = head ? a.ln_f_b : Ly->ln1_b;
+  const float *v2 = head ? a.fn_w : Ly->ln2_w, *v3 = head ? a.fn_b : Ly->ln2_b;
+  for (int arr = 0; arr < 4; arr++) {
+    const float *src = arr == 0 ? v0 : arr == 1 ? v1 : arr == 2 ? v2 : v3;
+    for (int off = 0; off < d; off += 256)  // 64 lanes x 4 floats per copy
+      if (off + lane * 4 < d) __builtin_amdgcn_global_load_lds(src + off + lane * 4, (lds_ptr)(lp + arr * d + off), 16, 0, 0);
   }
+  float *bl = lp + 4 * d;
+  auto rows = [&](const RowMap &m, const float *bias) {
+    for (int r0 = 0; r0 < m.rows; r0 += 64)
+      if (r0 + lane < m.rows) __builtin_amdgcn_global_load_lds(bias + m.row0 + r0 + lane, (lds_ptr)(bl + r0), 4, 0, 0);
+    bl += m.rows;
+  };
+  if (head) {
+    rows(mh, a.head.bias);
+    return;
+  }
+  rows(mq, Ly->attn.bias);
+  rows(mp, Ly->proj.bias);
+  rows(mf, Ly->fc.bias);
+  rows(mm, Ly->mproj.bias);
+}
+
+// Block-wide sum over the 1024 threads (same order on every block); red is this
+// reduction's own scratch, so one barrier suffices.
+__device__ inline float bsum(float v, float *red, int tid) {
+  v = wave64_sum(v);
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kThreads / 64; i++) t += red[i];
+  return t;
+}
+
+// LayerNorm (biased variance, eps 1e-5) of the LDS row x into the LDS row y (y may be x),
+// w and b in LDS, fused with the 16-element chunk sums of y that the GEMV consumes.
+// red holds 32 floats (two reductions' scratch).
+__device__ __forceinline__ void ln_chunks(const float *x, float *y, const float *w, const float *b, int n, float *xsum,
+                                 float *red, int tid) {
+  float s = 0.0f;
+  for (int i = tid; i < n; i += kThreads) s += x[i];
+  const float mean = bsum(s, red, tid) / (float)n;
+  float q = 0.0f;
+  for (int i = tid; i < n; i += kThreads) {
+    const float dv = x[i] - mean;
+    q += dv * dv;
+  }
+  const float var = bsum(q, red + 16, tid) / (float)n;
+  const float rstd = 1.0f / sqrtf(var + 1e-5f);
+  for (int base = 0; base < n; base += kThreads) {
+    const int i = base + tid;
+    const float v = i < n ? (x[i] - mean) * rstd * w[i] + b[i] : 0.0f;
+    if (i < n) y[i] = v;
+    // 16 consecutive threads hold one chunk
+    const float c = row16_sum(v);
+    if ((tid & 15) == 15 && i < n) xsum[i >> 4] = c;
+  }
+  __syncthreads();
 }
 
 struct PersistShared {
-  float red[16];
+  float red[32];
   int abort;
   int last;
-  float m_w[kComputeWaves], l_w[kComputeWaves];
+  float m_w[kLoadWaves], l_w[kLoadWaves];
 };
 
-template <int PT>
-__global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a) {
-  __shared__ PersistShared sh;
-  extern __shared__ float lds[];
+enum Role : int { kRolePoll = 0, kRolePub = 1, kRoleLoad = 2 };
+
+// The whole step as seen by one wave role.  The three instantiations execute the same
+// sequence of __syncthreads; each contains only its role's work, so the compiler allocates
+// registers per role (a role branch on a divergent condition would be linearised and make
+// every wave hold the registers of all roles).
+template <int PT, int ROLE>
+__device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, float *lds) {
+  constexpr bool poller = ROLE == kRolePoll, pub = ROLE == kRolePub, loader = ROLE == kRoleLoad;
   DecodeCtl *ctl = a.ctl;
-  if (ctl->done) return;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const bool poller = tid < kPollThreads;
-  const int cl = tid - kPollThreads;           // compute lane (when !poller)
-  const int cw = wave - kPollThreads / 64;     // compute wave (when !poller)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ll = tid - kLoadWave0 * 64;                                  // loader lane
+  const int lw = __builtin_amdgcn_readfirstlane((tid >> 6) - kLoadWave0);  // loader wave
   const int B = gridDim.x, b = blockIdx.x;
-  const int d = a.d, F = a.F, V = a.V, H = a.H, S = a.S;
+  const int d = a.d, F = a.F, H = a.H, S = a.S;
   const int tok = ctl->tok, pos = ctl->pos, vlen = ctl->valid_len;
   const uint32_t xstep = (uint32_t)ctl->xstep;
   const uint32_t ep0 = xstep * a.ep_stride + 1u;
   const int L = vlen + 1;  // keys including the row this step appends
   uint32_t *err = a.err;
 
-  // LDS: xin[xin_len] | xn[d] | xsum[xin_len/16] | part[part_len] | own[own_len] |
-  //      own_mid[own_len] | qs[64] | kn[64] | vn[64] | ow[12*64] | pp[S*66]
+  // LDS (floats): xin[xin_len] | xn[d] | xsum[xin_len/16] | part[part_len] | own[own_len] |
+  // own_mid[own_len] | out[out_len] | qs[64] | kn[64] | vn[64] | pp[S*66] |
+  // lp[2][lp_len] | kvs[2*3*576*4]; the host rounds every length to a multiple of 4
   float *xin = lds;
   float *xn = xin + a.xin_len;
   float *xsum = xn + d;
   float *part = xsum + a.xin_len / 16;
   float *own = part + a.part_len;
   float *own_mid = own + a.own_len;
-  float *qs = own_mid + a.own_len;
+  float *out = own_mid + a.own_len;
+  float *qs = out + a.out_len;
   float *kn = qs + 64;
   float *vn = kn + 64;
-  float *ow = vn + 64;
-  float *pp = ow + kComputeWaves * 64;
+  float *pp = vn + 64;
+  float *lpb = pp + a.pp_len;
+  float *kvs = lpb + 2 * a.lp_len;  // [2][kKeyPasses][576] x 16 bytes
 
   const RowMap m_qkv = rows_of(3 * d, d / 16, b, B);
   const RowMap m_proj = rows_of(d, d / 16, b, B);
   const RowMap m_fc = rows_of(F, d / 16, b, B);
   const RowMap m_mp = rows_of(d, F / 16, b, B);
-  const RowMap m_head = rows_of(V, d / 16, b, B);
+  const RowMap m_head = rows_of(a.V, d / 16, b, B);
+  // bias rows inside a layer's parameter buffer
+  const int bo_q = 4 * d, bo_p = bo_q + m_qkv.rows, bo_f = bo_p + m_proj.rows, bo_m = bo_f + m_fc.rows;
   const bool attn_block = b < H * S;
   const int ah = b / S, aj = b % S;
   const int j0 = (int)((long)L * aj / S), j1 = (int)((long)L * (aj + 1) / S);
-  const int kslot = cl >> 3, dsl = cl & 7;     // attention lane: key slot, 8-dim slice
 
-  if (tid == 0) {
-    sh.abort = 0;
-    sh.last = 0;
-  }
-
-  // ---- prologue: layer 0's weights in flight; the step embedding -------------------
+  // ---- prologue: layer 0's first two matrices in flight; embedding; parameters -------
   Slots<PT, kSlQkv> wq;
   Slots<PT, kSlProj> wp;
   Slots<PT, kSlFc> wf;
   Slots<PT, kSlMp> wm;
-  if (!poller) {
-    const DevLayer &L0 = a.layers[0];
-    load_slots<PT>(wq, L0.attn, m_qkv, cl);
-    load_slots<PT>(wp, L0.proj, m_proj, cl);
+  if (loader) {
+    load_slots<PT>(wq, a.layers[0].attn, m_qkv, ll);
+    load_slots<PT>(wp, a.layers[0].proj, m_proj, ll);
   }
-  for (int i = tid; i < d; i += kThreads) xin[i] = a.mel_emb[(size_t)tok * d + i] + a.mel_pos[(size_t)pos * d + i];
+  if (poller) {
+    for (int i = tid; i < d; i += kPollThreads)
+      xin[i] = gld<float>(a.mel_emb + (size_t)tok * d + i) + gld<float>(a.mel_pos + (size_t)pos * d + i);
+  }
+  if (pub) {
+    stage_params_dma(a, 0, lpb, m_qkv, m_proj, m_fc, m_mp, m_head, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
   __syncthreads();
-  for (int r = tid; r < m_proj.rows; r += kThreads) own[r] = xin[m_proj.row0 + r];
+  if (pub)
+    for (int r = lane; r < m_proj.rows; r += 64) own[r] = xin[m_proj.row0 + r];
 
   for (int l = 0; l < a.n_layer; l++) {
+    // thread index re-derived opaquely per layer: per-thread LDS addresses are recomputed
+    // in each layer instead of being hoisted out of the loop and held for the whole step
+    int T = tid;
+    asm volatile("" : "+v"(T));
+    const int lane = T & 63, ll = T - kLoadWave0 * 64;
+    const int kslot = ll >> 3, dsl = ll & 7;  // attention loader lane: key slot, 8-dim slice
     const DevLayer &Ly = a.layers[l];
     const uint32_t ep = ep0 + (uint32_t)l * 8u;
+    const float *lp = lpb + (l & 1) * a.lp_len;
     // ---------------- P1: LN1, QKV rows; K/V rows into the cache --------------------
     if (l > 0) {
-      if (poller && !poll_words(a.x_x, d, ep - 8u + 6u, xin, err)) sh.abort = 1;
+      if (poller && !poll_words<kPollD>(a.x_x, d, ep - 8u + 6u, xin, err, T)) sh.abort = 1;
       __syncthreads();
       if (sh.abort) return;
     }
-    layernorm_lds_inplace_to<kThreads>(xin, xn, Ly.ln1_w, Ly.ln1_b, d, sh.red);
-    chunk_sums(xn, d, xsum);
+    ln_chunks(xin, xn, lp, lp + d, d, xsum, sh.red, T);
+    if (loader) dot_slots(wq, m_qkv, xn, xsum, part, ll);
     __syncthreads();
-    if (!poller) {
-      dot_slots(wq, m_qkv, xn, xsum, part, cl);
-      load_slots<PT>(wf, Ly.fc, m_fc, cl);
-    }
+    if (loader) row_sums(m_qkv, part, lp + bo_q, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
-    if (!poller) {
-      row_sums(m_qkv, part, Ly.attn.bias, cw, lane, [&](int r, float v) {
+    if (pub) {
+      for (int r = lane; r < m_qkv.rows; r += 64) {
         const int R = m_qkv.row0 + r;
+        const float v = out[r];
         ll_store(a.x_qkv + R, ep + 1u, v);
         if (R >= d) {
           const int idx = R < 2 * d ? R - d : R - 2 * d;
@@ -294,47 +454,55 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
           uint16_t *cache = static_cast<uint16_t *>(R < 2 * d ? a.kc : a.vc);
           cache[(((size_t)l * H + h) * a.max_seq + vlen) * 64 + e] = (uint16_t)float_to_bf16_bits(v);
         }
-      });
+      }
     }
+    // the next layer's parameters: copied by the publisher (a poller's copies would delay
+    // its next poll, which completes in issue order); it waits for them after its P4
+    // stores, well before the next layer reads them
+    if (pub) stage_params_dma(a, l + 1, lpb + ((l + 1) & 1) * a.lp_len, m_qkv, m_proj, m_fc, m_mp, m_head, lane);
+    // fc weights: needed after the attention, c_proj and an exchange (the longest lead)
+    if (loader) load_slots<PT>(wf, Ly.fc, m_fc, ll);
     // ---------------- P2: attention split of head ah over keys [j0, j1) ----------------
     if (attn_block) {
-      // K/V of the split's cached rows (the appended row comes from the exchange);
-      // loaded before waiting for the query
-      uint4 kreg[kKeyPasses], vreg[kKeyPasses];
-      if (!poller) {
+      // cached K/V rows of the split (the appended row comes from the exchange), copied
+      // straight into LDS (no registers) before the query arrives; out-of-split slots read
+      // row 0.  Lane ll of pass ps lands at kvs[(ps*576 + ll)*4], K passes then V passes.
+      if (loader) {
         const size_t hb = ((size_t)l * H + ah) * a.max_seq * 64;
         const uint16_t *kh = static_cast<const uint16_t *>(a.kc) + hb;
         const uint16_t *vh = static_cast<const uint16_t *>(a.vc) + hb;
 #pragma unroll
         for (int ps = 0; ps < kKeyPasses; ps++) {
-          const int key = j0 + kslot + kKeySlots * ps;
-          if (key < j1 && key < L - 1) {
-            kreg[ps] = *reinterpret_cast<const uint4 *>(kh + (size_t)key * 64 + dsl * 8);
-            vreg[ps] = *reinterpret_cast<const uint4 *>(vh + (size_t)key * 64 + dsl * 8);
-          } else {
-            kreg[ps] = make_uint4(0, 0, 0, 0);
-            vreg[ps] = make_uint4(0, 0, 0, 0);
-          }
+          int key = j0 + kslot + kKeySlots * ps;
+          key = key < j1 && key < L - 1 ? key : 0;
+          float *wk = kvs + (ps * kLoadThreads + lw * 64) * 4;
+          float *wv = kvs + ((kKeyPasses + ps) * kLoadThreads + lw * 64) * 4;
+          __builtin_amdgcn_global_load_lds(kh + (size_t)key * 64 + dsl * 8, (__attribute__((address_space(3))) void *)wk,
+                                           16, 0, 0);
+          __builtin_amdgcn_global_load_lds(vh + (size_t)key * 64 + dsl * 8, (__attribute__((address_space(3))) void *)wv,
+                                           16, 0, 0);
         }
       }
       if (poller) {
-        bool ok = poll_words(a.x_qkv + ah * 64, 64, ep + 1u, qs, err);
+        bool ok = poll_words<1>(a.x_qkv + ah * 64, 64, ep + 1u, qs, err, T);
         if (ok && j1 == L) {  // this split holds the appended row
-          ok = poll_words(a.x_qkv + d + ah * 64, 64, ep + 1u, kn, err) &&
-               poll_words(a.x_qkv + 2 * d + ah * 64, 64, ep + 1u, vn, err);
+          ok = poll_words<1>(a.x_qkv + d + ah * 64, 64, ep + 1u, kn, err, T) &&
+               poll_words<1>(a.x_qkv + 2 * d + ah * 64, 64, ep + 1u, vn, err, T);
         }
         if (!ok) sh.abort = 1;
       }
       __syncthreads();
       if (sh.abort) return;
       // the appended row as the cache stores it (bf16)
-      if (tid < 64) {
-        kn[tid] = bf16_bits_to_float(float_to_bf16_bits(kn[tid]));
-        vn[tid] = bf16_bits_to_float(float_to_bf16_bits(vn[tid]));
+      if (pub) {
+        kn[lane] = bf16_bits_to_float(float_to_bf16_bits(kn[lane]));
+        vn[lane] = bf16_bits_to_float(float_to_bf16_bits(vn[lane]));
       }
       __syncthreads();
       float sc[kKeyPasses];
-      if (!poller) {
+      if (loader) {
+        // the copies above are the loaders' latest vector-memory operations
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         float mloc = -INFINITY;
 #pragma unroll
         for (int ps = 0; ps < kKeyPasses; ps++) {
@@ -345,7 +513,8 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
 #pragma unroll
               for (int e = 0; e < 8; e++) pd += qs[dsl * 8 + e] * kn[dsl * 8 + e];
             } else {
-              const uint32_t w[4] = {kreg[ps].x, kreg[ps].y, kreg[ps].z, kreg[ps].w};
+              const uint4 kq = *reinterpret_cast<const uint4 *>(kvs + (ps * kLoadThreads + ll) * 4);
+              const uint32_t w[4] = {kq.x, kq.y, kq.z, kq.w};
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 pd += qs[dsl * 8 + 2 * e] * __uint_as_float(w[e] << 16);
@@ -353,19 +522,22 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
               }
             }
           }
-          pd += __shfl_xor(pd, 1, 64);
-          pd += __shfl_xor(pd, 2, 64);
-          pd += __shfl_xor(pd, 4, 64);
+          // sum over the key's 8 lanes, to all 8: xor 1 and 2 within quads, then each quad
+          // adds its neighbour quad (row_shr:4 into lanes 4-7 / 12-15, row_shl:4 into 0-3 /
+          // 8-11); a + b == b + a, so all 8 lanes hold the same value
+          pd += dpp_f<0xB1, 0xf, 0xf>(pd, 0.0f);  // quad_perm [1,0,3,2]
+          pd += dpp_f<0x4E, 0xf, 0xf>(pd, 0.0f);  // quad_perm [2,3,0,1]
+          pd = pd + dpp_f<0x114, 0xf, 0xa>(pd, 0.0f) + dpp_f<0x104, 0xf, 0x5>(pd, 0.0f);
           sc[ps] = key < j1 ? pd * 0.125f : -INFINITY;
           mloc = fmaxf(mloc, sc[ps]);
         }
-        mloc = wave_max(mloc);
-        if (lane == 0) sh.m_w[cw] = mloc;
+        mloc = wave64_max(mloc);
+        if (lane == 0) sh.m_w[lw] = mloc;
       }
       __syncthreads();
       float M = -INFINITY;
-      for (int w = 0; w < kComputeWaves; w++) M = fmaxf(M, sh.m_w[w]);
-      if (!poller) {
+      for (int w = 0; w < kLoadWaves; w++) M = fmaxf(M, sh.m_w[w]);
+      if (loader) {
         float o8[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) o8[e] = 0.0f;
@@ -380,7 +552,8 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
 #pragma unroll
               for (int e = 0; e < 8; e++) o8[e] += p * vn[dsl * 8 + e];
             } else {
-              const uint32_t w[4] = {vreg[ps].x, vreg[ps].y, vreg[ps].z, vreg[ps].w};
+              const uint4 vq = *reinterpret_cast<const uint4 *>(kvs + ((kKeyPasses + ps) * kLoadThreads + ll) * 4);
+              const uint32_t w[4] = {vq.x, vq.y, vq.z, vq.w};
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 o8[2 * e] += p * __uint_as_float(w[e] << 16);
@@ -389,41 +562,46 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
             }
           }
         }
-        lsum = wave_sum(lsum);
+        lsum = wave64_sum(lsum);
+        // lanes i and i+8 of a 16-lane row share a dimension slice: fold them (row_ror:8),
+        // then the low half of every row writes its 8 dimensions; the K staging area is
+        // free since the scores are done (the barrier above)
+        float *ow2 = kvs;  // [9 waves][4 rows][64 dims]
 #pragma unroll
-        for (int off = 8; off < 64; off <<= 1) {
-#pragma unroll
-          for (int e = 0; e < 8; e++) o8[e] += __shfl_xor(o8[e], off, 64);
+        for (int e = 0; e < 8; e++) o8[e] += dpp_f<0x128, 0xf, 0xf>(o8[e], 0.0f);
+        if ((lane & 15) < 8) {
+          float *dst = ow2 + (lw * 4 + (lane >> 4)) * 64 + dsl * 8;
+          *reinterpret_cast<float4 *>(dst) = make_float4(o8[0], o8[1], o8[2], o8[3]);
+          *reinterpret_cast<float4 *>(dst + 4) = make_float4(o8[4], o8[5], o8[6], o8[7]);
         }
-        if (lane < 8) {
-#pragma unroll
-          for (int e = 0; e < 8; e++) ow[cw * 64 + lane * 8 + e] = o8[e];
-        }
-        if (lane == 0) sh.l_w[cw] = lsum;
+        if (lane == 0) sh.l_w[lw] = lsum;
       }
       __syncthreads();
-      // block partial -> exchange; the last split of the head to finish combines
-      if (tid < 64) {
+      // block partial -> exchange (publisher); the split counter (a poller, which has no
+      // stores in flight) names the last split of the head to finish, which combines
+      if (pub) {
         float osum = 0.0f;
-        for (int w = 0; w < kComputeWaves; w++) osum += ow[w * 64 + tid];
+        for (int w = 0; w < kLoadWaves * 4; w++) osum += kvs[w * 64 + lane];
         uint64_t *pw = a.x_part + ((size_t)ah * S + aj) * 66;
-        ll_store(pw + 2 + tid, ep + 2u, osum);
-        if (tid == 0) {
+        ll_store(pw + 2 + lane, ep + 2u, osum);
+        if (lane == 0) {
           float lt = 0.0f;
-          for (int w = 0; w < kComputeWaves; w++) lt += sh.l_w[w];
+          for (int w = 0; w < kLoadWaves; w++) lt += sh.l_w[w];
           ll_store(pw, ep + 2u, M);
           ll_store(pw + 1, ep + 2u, lt);
-          // wrapping device-scope counter: cycles 0..S-1, so the S-th arrival reads S-1
-          const uint32_t old = atomicInc(a.cnt + ah * kCntStride, (uint32_t)(S - 1));
-          sh.last = old == (uint32_t)(S - 1);
         }
+      }
+      if (poller && T == 0) {
+        // wrapping device-scope counter: cycles 0..S-1, so the S-th arrival reads S-1
+        const uint32_t old = atomicInc(a.cnt + ah * kCntStride, (uint32_t)(S - 1));
+        sh.last = old == (uint32_t)(S - 1);
       }
       __syncthreads();
       if (sh.last) {
-        if (poller && !poll_words(a.x_part + (size_t)ah * S * 66, S * 66, ep + 2u, pp, err)) sh.abort = 1;
+        if (poller && !poll_words<2>(a.x_part + (size_t)ah * S * 66, S * 66, ep + 2u, pp, err, T)) sh.abort = 1;
         __syncthreads();
         if (sh.abort) return;
-        if (tid < 64) {
+        if (pub) {
           float Mg = -INFINITY;
           for (int s = 0; s < S; s++) Mg = fmaxf(Mg, pp[s * 66]);
           float den = 0.0f, num = 0.0f;
@@ -431,88 +609,105 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
             if (pp[s * 66] == -INFINITY) continue;
             const float f = __expf(pp[s * 66] - Mg);
             den += pp[s * 66 + 1] * f;
-            num += pp[s * 66 + 2 + tid] * f;
+            num += pp[s * 66 + 2 + lane] * f;
           }
-          ll_store(a.x_attn + ah * 64 + tid, ep + 3u, num / den);
+          ll_store(a.x_attn + ah * 64 + lane, ep + 3u, num / den);
         }
       }
     }
     // ---------------- P3: c_proj rows + residual ------------------------------------
-    if (poller && !poll_words(a.x_attn, d, ep + 3u, xin, err)) sh.abort = 1;
+    if (poller && !poll_words<kPollD>(a.x_attn, d, ep + 3u, xin, err, T, xsum)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    chunk_sums(xin, d, xsum);
+    if (loader) dot_slots(wp, m_proj, xin, xsum, part, ll);
     __syncthreads();
-    if (!poller) {
-      dot_slots(wp, m_proj, xin, xsum, part, cl);
-      load_slots<PT>(wm, Ly.mproj, m_mp, cl);
-    }
-    __syncthreads();
-    if (!poller) {
-      row_sums(m_proj, part, Ly.proj.bias, cw, lane, [&](int r, float v) {
+    if (loader)
+      row_sums(m_proj, part, lp + bo_p, lw, lane, [&](int r, float v) {
         const float xm = own[r] + v;
         own_mid[r] = xm;
-        ll_store(a.x_mid + m_proj.row0 + r, ep + 4u, xm);
+        out[r] = xm;
       });
-    }
+    __syncthreads();
+    if (pub)
+      for (int r = lane; r < m_proj.rows; r += 64) ll_store(a.x_mid + m_proj.row0 + r, ep + 4u, out[r]);
+    // prefetches are issued once the phase's outputs are out (issuing them earlier delays
+    // the row sums behind the memory pipeline)
+    if (loader) load_slots<PT>(wm, Ly.mproj, m_mp, ll);
     // ---------------- P4: LN2, c_fc rows + GELU ------------------------------------
-    if (poller && !poll_words(a.x_mid, d, ep + 4u, xin, err)) sh.abort = 1;
+    if (poller && !poll_words<kPollD>(a.x_mid, d, ep + 4u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    layernorm_lds_inplace_to<kThreads>(xin, xn, Ly.ln2_w, Ly.ln2_b, d, sh.red);
-    chunk_sums(xn, d, xsum);
+    ln_chunks(xin, xn, lp + 2 * d, lp + 3 * d, d, xsum, sh.red, T);
+    if (loader) dot_slots(wf, m_fc, xn, xsum, part, ll);
     __syncthreads();
-    if (!poller) {
-      dot_slots(wf, m_fc, xn, xsum, part, cl);
-      if (l + 1 < a.n_layer) load_slots<PT>(wq, a.layers[l + 1].attn, m_qkv, cl);
-    }
+    if (loader) row_sums(m_fc, part, lp + bo_f, lw, lane, [&](int r, float v) { out[r] = gelu_tanh(v); });
     __syncthreads();
-    if (!poller) {
-      row_sums(m_fc, part, Ly.fc.bias, cw, lane,
-               [&](int r, float v) { ll_store(a.x_f + m_fc.row0 + r, ep + 5u, gelu_tanh(v)); });
+    if (pub) {
+      for (int r = lane; r < m_fc.rows; r += 64) ll_store(a.x_f + m_fc.row0 + r, ep + 5u, out[r]);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next layer's parameter copies
     }
+    if (loader && l + 1 < a.n_layer) load_slots<PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
     // ---------------- P5: mlp c_proj rows + residual ---------------------------------
-    if (poller && !poll_words(a.x_f, F, ep + 5u, xin, err)) sh.abort = 1;
+    if (poller && !poll_words<kPollF>(a.x_f, F, ep + 5u, xin, err, T, xsum)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    chunk_sums(xin, F, xsum);
+    if (loader) dot_slots(wm, m_mp, xin, xsum, part, ll);
     __syncthreads();
-    if (!poller) {
-      dot_slots(wm, m_mp, xin, xsum, part, cl);
-      if (l + 1 < a.n_layer) load_slots<PT>(wp, a.layers[l + 1].proj, m_proj, cl);
-    }
-    __syncthreads();
-    if (!poller) {
-      row_sums(m_mp, part, Ly.mproj.bias, cw, lane, [&](int r, float v) {
+    if (loader)
+      row_sums(m_mp, part, lp + bo_m, lw, lane, [&](int r, float v) {
         const float xo = own_mid[r] + v;
         own[r] = xo;
-        ll_store(a.x_x + m_mp.row0 + r, ep + 6u, xo);
+        out[r] = xo;
       });
-    }
+    __syncthreads();
+    if (pub)
+      for (int r = lane; r < m_mp.rows; r += 64) ll_store(a.x_x + m_mp.row0 + r, ep + 6u, out[r]);
+    if (loader && l + 1 < a.n_layer) load_slots<PT>(wp, a.layers[l + 1].proj, m_proj, ll);
   }
   // ---------------- head: ln_f, final_norm, mel_head rows -> logits ------------------
   {
     Slots<PT, kSlHead> wh;
-    if (!poller) load_slots<PT>(wh, a.head, m_head, cl);
+    if (loader) load_slots<PT>(wh, a.head, m_head, ll);
     const uint32_t ep = ep0 + (uint32_t)(a.n_layer - 1) * 8u;
-    if (poller && !poll_words(a.x_x, d, ep + 6u, xin, err)) sh.abort = 1;
+    const float *lp = lpb + (a.n_layer & 1) * a.lp_len;
+    if (poller && !poll_words<kPollD>(a.x_x, d, ep + 6u, xin, err, tid)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    layernorm_lds_inplace_to<kThreads>(xin, xn, a.ln_f_w, a.ln_f_b, d, sh.red);
-    layernorm_lds_inplace<kThreads>(xn, a.fn_w, a.fn_b, d, sh.red);
-    chunk_sums(xn, d, xsum);
+    ln_chunks(xin, xn, lp, lp + d, d, xsum, sh.red, tid);
+    ln_chunks(xn, xn, lp + 2 * d, lp + 3 * d, d, xsum, sh.red, tid);
+    if (loader) dot_slots(wh, m_head, xn, xsum, part, ll);
     __syncthreads();
-    if (!poller) dot_slots(wh, m_head, xn, xsum, part, cl);
+    if (loader) row_sums(m_head, part, lp + 4 * d, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
-    if (!poller)
-      row_sums(m_head, part, a.head.bias, cw, lane, [&](int r, float v) { a.logits[m_head.row0 + r] = v; });
+    if (pub) {
+      for (int r = lane; r < m_head.rows; r += 64) a.logits[m_head.row0 + r] = out[r];
+      // Block 0 closes the step.  Every block read the control block at its start, before
+      // its first exchange word, and block 0 gets here only after every block's last
+      // exchange.
+      if (b == 0 && lane == 0) {
+        ctl->valid_len = vlen + 1;
+        ctl->xstep = (int32_t)(xstep + 1u);
+      }
+    }
   }
-  // Block 0 closes the step.  Every block read the control block at its start, before its
-  // first exchange word, and block 0 gets here only after every block's last exchange.
-  if (b == 0 && tid == 0) {
-    ctl->valid_len = vlen + 1;
-    ctl->xstep = (int32_t)(xstep + 1u);
+}
+
+template <int PT>
+__global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a) {
+  __shared__ PersistShared sh;
+  extern __shared__ float lds[];
+  if (a.ctl->done) return;
+  if (threadIdx.x == 0) {
+    sh.abort = 0;
+    sh.last = 0;
   }
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (wave >= kLoadWave0)
+    run<PT, kRoleLoad>(a, sh, lds);
+  else if (wave == kPubWave)
+    run<PT, kRolePub>(a, sh, lds);
+  else
+    run<PT, kRolePoll>(a, sh, lds);
 }
 
 }  // namespace
@@ -523,7 +718,7 @@ bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int
   if (S < 1) return false;
   if ((max_seq + S - 1) / S > kKeySlots * kKeyPasses) return false;
   auto fits = [&](int N, int C, int slots) {
-    return (long)((N + B - 1) / B) * C <= (long)slots * kComputeThreads;
+    return (long)((N + B - 1) / B) * C <= (long)slots * kLoadThreads;
   };
   if (!fits(3 * d, d / 16, kSlQkv) || !fits(d, d / 16, kSlProj) || !fits(F, d / 16, kSlFc) ||
       !fits(d, F / 16, kSlMp) || !fits(V, d / 16, kSlHead))
@@ -533,8 +728,8 @@ bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int
 }
 
 size_t persist_lds_bytes(const PersistArgs &a) {
-  const size_t f = (size_t)a.xin_len + a.d + a.xin_len / 16 + a.part_len + 2 * (size_t)a.own_len + 3 * 64 +
-                   kComputeWaves * 64 + (size_t)a.S * 66;
+  const size_t f = (size_t)a.xin_len + a.d + a.xin_len / 16 + a.part_len + 2 * (size_t)a.own_len + a.out_len +
+                   3 * 64 + a.pp_len + 2 * (size_t)a.lp_len + 2 * kKeyPasses * kLoadThreads * 4;
   return f * sizeof(float);
 }
 

@@ -456,10 +456,15 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     a.V = V;
     a.S = S;
     a.B = B;
+    auto r4 = [](int n) { return (n + 3) & ~3; };
+    auto rows = [&](int N) { return (N + B - 1) / B; };
+    const int rq = rows(3 * d), rp = rows(d), rf = rows(F), rh = rows(V);
     a.xin_len = std::max(d, F);
-    auto cap = [&](int N, int C) { return ((N + B - 1) / B) * C; };
-    a.part_len = std::max({cap(3 * d, d / 16), cap(d, d / 16), cap(F, d / 16), cap(d, F / 16), cap(V, d / 16)});
-    a.own_len = (d + B - 1) / B;
+    a.part_len = r4(std::max({rq * (d / 16), rp * (d / 16), rf * (d / 16), rp * (F / 16), rh * (d / 16)}));
+    a.own_len = r4(rp);
+    a.out_len = r4(std::max({rq, rp, rf, rh}));
+    a.pp_len = r4(S * 66);
+    a.lp_len = r4(4 * d + std::max(rq + rp + rf + rp, rh));
   }
   bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
   if (ok) {

@@ -26,7 +26,8 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libitts_hip.so")
+# the in-tree build, unless ITTS_HIP_LIB names another build of the same library
+LIB_PATH = os.environ.get("ITTS_HIP_LIB") or os.path.join(os.path.dirname(_HERE), "lib", "libitts_hip.so")
 
 ITTS_OK, ITTS_E_VALIDATION, ITTS_E_WEIGHT, ITTS_E_DEVICE, ITTS_E_CAPACITY, ITTS_E_INTERNAL = range(6)
 ITTS_F16, ITTS_F32, ITTS_BF16 = 1, 2, 3
