@@ -93,9 +93,6 @@ hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipS
 // Persistent decode step (kernels_persist.hip): one cooperative launch of B blocks
 // (one per CU) runs a whole decode step.  Exchange words are (epoch << 32 | fp32 bits).
 constexpr int kCntStride = 32;  // one 128-byte line per head counter
-// Every exchange array is followed by this many readable words (a polling wave reads up
-// to 63 words past the end of what it needs).
-constexpr int kPersistPad = 64;
 struct PersistArgs {
   const DevLayer *layers;  // device array [n_layer]
   int n_layer, d, H, F, V, S, B;
@@ -105,7 +102,8 @@ struct PersistArgs {
   void *kc, *vc;           // bf16 cache bases [n_layer][H][max_seq][64]
   int max_seq;
   DecodeCtl *ctl;
-  uint64_t *x_x, *x_qkv, *x_part, *x_attn, *x_mid, *x_f;  // [d] [3d] [H*S*66] [d] [d] [F]
+  // exchange arrays of 16-byte words (three values and an epoch), 16-byte aligned
+  void *x_x, *x_qkv, *x_part, *x_attn, *x_mid, *x_f;
   uint32_t *cnt;           // [H * kCntStride] split counters (wrap at S; start at 0)
   uint32_t *err;           // nonzero after a timed-out wait
   float *logits;           // [V]
@@ -118,6 +116,9 @@ struct PersistArgs {
 bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int *S);
 constexpr size_t kPersistMaxLds = 150 * 1024;
 size_t persist_lds_bytes(const PersistArgs &a);
+// 16-byte words of the exchange arrays x_x, x_qkv, x_part, x_attn, x_mid, x_f: total, and
+// each array's offset in off[6].
+size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]);
 // Blocks of the persistent kernel that fit on one compute unit with `lds` bytes of LDS.
 hipError_t persist_blocks_per_cu(int ptype, size_t lds, int *blocks);
 hipError_t launch_decode_persist(PersistArgs a, int ptype, hipStream_t s);

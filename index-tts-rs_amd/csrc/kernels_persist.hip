@@ -4,14 +4,15 @@
 // Why persistent.  A batch-1 step is a chain of ~120 dependent GEMV/attention phases over
 // small matrices.  As separate kernels each phase pays the launch floor (~2 us) plus the
 // loaded HBM latency (~1.7 us) before its first weight byte arrives.  Here every block
-// keeps its share of each matrix in registers, loaded two matrices ahead of use, so HBM
-// latency overlaps the dependency chain; what is left per phase is the exchange of the
-// phase's output vector between blocks.
+// keeps its share of each matrix in registers, loaded ahead of use, so HBM latency
+// overlaps the dependency chain; what is left per phase is the exchange of the phase's
+// output vector between blocks.
 //
-// Exchange.  Every cross-block value travels as one 64-bit word (epoch << 32 | fp32 bits)
-// written and read with device-scope relaxed atomics: a reader polls the words it needs
-// until each carries the phase's epoch, so no fence or grid barrier is needed and a stale
-// word is never mistaken for a fresh one.  Epoch of (step s, layer l, phase p):
+// Exchange.  Values travel in 16-byte words: three fp32 values and an epoch, written by
+// one lane with one store and read with one load, both device-coherent.  A reader polls
+// the words it needs until each carries the phase's epoch, so no fence or grid barrier is
+// needed and a stale word is never taken for a fresh one.  A producer's values form one
+// segment of ceil(len/3) words.  Epoch of (step s, layer l, phase p):
 // s * 8 * (n_layer + 1) + 8 * l + p + 1, with s from the control block.  A word is
 // rewritten only after every block has consumed it: the next write of any array depends
 // on every block's output of a later phase.
@@ -21,14 +22,13 @@
 // an unrelated operation, each wave kind issues one kind of global access:
 //   pollers  (waves 0-5)  : loads only - exchange polls, the embedding;
 //   publisher (wave 6)    : exchange words, K/V cache rows and logits (stores), and the
-//                           next layer's parameters (loads it waits for, while no other
-//                           work depends on it);
-//   loaders  (waves 7-15) : loads only, all unconditional - the weight slices (two
-//                           matrices ahead) and the attention K/V rows; they compute
-//                           the dot products and row sums in LDS.
-// Every wave takes part in every __syncthreads, which on gfx950 waits for LDS traffic
-// only.  LayerNorm parameters and bias rows reach the loaders through LDS, staged one
-// layer ahead (double buffer).
+//                           next layer's parameters (LDS-DMA copies it waits for where it
+//                           has slack);
+//   loaders  (waves 7-15) : loads only, all unconditional - the weight slices (ahead of
+//                           use) and the attention K/V rows (LDS-DMA); they compute the
+//                           dot products and row sums in LDS.
+// Each role is its own instantiation of the step program (run<PT, ROLE>), all executing
+// the same sequence of __syncthreads, which on gfx950 waits for LDS traffic only.
 //
 // Ownership.  For a matrix with N rows, block b owns rows [N*b/B, N*(b+1)/B).  A block's
 // rows of c_proj and of the MLP's c_proj coincide, so it keeps its slice of the residual
@@ -54,122 +54,43 @@ constexpr int kLoadWaves = 9;
 constexpr int kLoadThreads = kLoadWaves * 64;  // waves 7-15
 constexpr int kKeySlots = kLoadThreads / 8;    // attention: 8 lanes per key
 constexpr int kKeyPasses = 3;                  // keys per split <= kKeySlots * kKeyPasses
-// exchange words per poller lane in flight: one batch covers a d_model vector (1280) or
-// the MLP vector (5120) of the full-size decoder
-constexpr int kPollD = 4, kPollF = 14;
 constexpr long kSpinLimit = 1L << 21;
-static_assert(kPollThreads % 64 == 0, "pollers are whole waves");
-static_assert(kPersistPad >= 64, "a polling wave may read up to 63 words past n");
+constexpr int kPartVals = 66;                  // attention partial: max, denominator, 64 outputs
+constexpr int kPartWords = (kPartVals + 2) / 3;
+constexpr int kHeadWords = (64 + 2) / 3;
 // 16-byte code chunks per loader lane (rows per block x chunks per row / 576, rounded up)
 // for the full-size decoder on 256 blocks
 constexpr int kSlQkv = 3, kSlProj = 1, kSlFc = 3, kSlMp = 3, kSlHead = 5;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct RowMap {
   int row0, rows, C;  // first row, row count, 16-byte chunks per row
 };
 
+__device__ inline int row_start(int N, int b, int B) { return (int)((long)N * b / B); }
 __device__ inline RowMap rows_of(int N, int C, int b, int B) {
-  const int r0 = (int)((long)N * b / B), r1 = (int)((long)N * (b + 1) / B);
-  return RowMap{r0, r1 - r0, C};
+  const int r0 = row_start(N, b, B);
+  return RowMap{r0, row_start(N, b + 1, B) - r0, C};
 }
+// The block whose rows contain row r: the largest b with row_start(N, b, B) <= r.
+__device__ inline int block_of(int N, int r, int B) { return (int)(((long)(r + 1) * B - 1) / N); }
+__device__ inline int words_for(int n) { return (n + 2) / 3; }
+// i / d for 0 <= i < 2^16 and 1 <= d <= 2^15: one multiply-high by m = floor((2^32-1)/d) + 1.
+// i*m/2^32 exceeds i/d by i*(m - 2^32/d)/2^32 < i/2^32, below the 1/d gap to the next
+// integer for these ranges, so the floor is exact.
+// d == 1 would need m = 2^32: it is kept as m = 0 and divides by returning i.
+struct FastDiv {
+  uint32_t m;
+  __device__ explicit FastDiv(int d) : m(d == 1 ? 0u : 0xffffffffu / (uint32_t)d + 1u) {}
+  __device__ int operator()(int i) const { return m ? (int)__umulhi((uint32_t)i, m) : i; }
+};
 
-__device__ inline void ll_store(uint64_t *p, uint32_t ep, float v) {
-  __hip_atomic_store(p, ((uint64_t)ep << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline uint64_t ll_load(const uint64_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ inline uint32_t ld_u32(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-// Cross-lane reductions with DPP (ALU row shifts and broadcasts, no LDS round trip).  They
-// need every lane of the wave active.  Fixed order, so every block reduces identically.
-template <int CTRL, int ROW_MASK, int BANK_MASK>
-__device__ inline float dpp_f(float v, float old) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
-}
-// Inclusive scan within each row of 16 lanes: lane 15 of a row holds the row's sum.
-__device__ inline float row16_sum(float x) {
-  x += dpp_f<0x111, 0xf, 0xf>(x, 0.0f);  // row_shr:1
-  x += dpp_f<0x112, 0xf, 0xf>(x, 0.0f);  // row_shr:2
-  x += dpp_f<0x114, 0xf, 0xe>(x, 0.0f);  // row_shr:4, lanes 4-15
-  x += dpp_f<0x118, 0xf, 0xc>(x, 0.0f);  // row_shr:8, lanes 8-15
-  return x;
-}
-// Sum over the wave, returned to every lane.
-__device__ inline float wave64_sum(float x) {
-  x = row16_sum(x);
-  x += dpp_f<0x142, 0xa, 0xf>(x, 0.0f);  // row_bcast:15 into rows 1, 3
-  x += dpp_f<0x143, 0xc, 0xf>(x, 0.0f);  // row_bcast:31 into rows 2, 3
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
-// Max over the wave, returned to every lane.
-__device__ inline float wave64_max(float x) {
-  const float ni = -INFINITY;
-  x = fmaxf(x, dpp_f<0x111, 0xf, 0xf>(x, ni));
-  x = fmaxf(x, dpp_f<0x112, 0xf, 0xf>(x, ni));
-  x = fmaxf(x, dpp_f<0x114, 0xf, 0xe>(x, ni));
-  x = fmaxf(x, dpp_f<0x118, 0xf, 0xc>(x, ni));
-  x = fmaxf(x, dpp_f<0x142, 0xa, 0xf>(x, ni));
-  x = fmaxf(x, dpp_f<0x143, 0xc, 0xf>(x, ni));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
-
-// Pollers: read n exchange words of epoch ep into dst (LDS).  A wave issues a batch load
-// only when its first lane's word is in range (a wave-uniform test), so lanes read at
-// most 63 words past n; the exchange arrays carry that padding.  False on timeout or
-// when another block raised the error word.
-template <int NB>
-__device__ __forceinline__ bool poll_words(const uint64_t *src, int n, uint32_t ep, float *dst, uint32_t *err, int t,
-                           float *xsum = nullptr) {
-  const int wb = t & ~63;
-  for (int base = 0; base < n; base += NB * kPollThreads) {
-    uint64_t w[NB];
-    long spins = 0;
-    while (true) {
-      // lane offset made opaque per spin: one base register instead of a hoisted 64-bit
-      // address per word and call site
-      uint32_t to = (uint32_t)(base + t) * 8u;
-      asm volatile("" : "+v"(to));
-      const uint64_t *p = reinterpret_cast<const uint64_t *>(reinterpret_cast<const char *>(src) + to);
-#pragma unroll
-      for (int k = 0; k < NB; k++) {
-        w[k] = 0;
-        if (base + wb + k * kPollThreads < n) w[k] = ll_load(p + k * kPollThreads);
-      }
-      bool all = true;
-#pragma unroll
-      for (int k = 0; k < NB; k++)
-        all = all && (base + t + k * kPollThreads >= n || (uint32_t)(w[k] >> 32) == ep);
-      if (__all(all)) break;
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return false;
-      }
-      if ((spins & 63) == 0 && ld_u32(err) != 0) return false;
-      __builtin_amdgcn_s_sleep(1);
-    }
-#pragma unroll
-    for (int k = 0; k < NB; k++) {
-      const int i = base + t + kPollThreads * k;
-      const float v = i < n ? __uint_as_float((uint32_t)w[k]) : 0.0f;
-      if (i < n) dst[i] = v;
-      if (xsum) {
-        // 16 consecutive lanes hold 16 consecutive words (kPollThreads is a multiple of
-        // 16): their sum is the chunk sum the GEMV consumes
-        const float c = row16_sum(v);
-        if ((t & 15) == 15 && i < n) xsum[i >> 4] = c;
-      }
-    }
-  }
-  return true;
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Load through the global address space.  Pointers read from the layer table are generic
 // to the compiler, and a generic (flat) load also counts against the LDS wait counter, so
@@ -179,6 +100,124 @@ __device__ inline T gld(const void *p) {
   return *(const __attribute__((address_space(1))) T *)p;
 }
 
+// ---- exchange words --------------------------------------------------------------------
+// One device-coherent 16-byte store: values a, b, c and the epoch in the last dword.
+__device__ inline void xstore(u32x4 *p, float a, float b, float c, uint32_t ep) {
+  const u32x4 v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), ep};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+
+// K device-coherent 16-byte loads in flight together, then one wait: the loads are issued
+// in one asm block so that the results are read only after the wait.
+template <int K>
+__device__ inline void xload(u32x4 (&w)[K], const u32x4 *const (&p)[K]);
+template <>
+__device__ inline void xload<1>(u32x4 (&w)[1], const u32x4 *const (&p)[1]) {
+  asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(w[0]) : "v"(p[0]) : "memory");
+}
+template <>
+__device__ inline void xload<2>(u32x4 (&w)[2], const u32x4 *const (&p)[2]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %2, off sc1\n\t"
+      "global_load_dwordx4 %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1])
+      : "v"(p[0]), "v"(p[1])
+      : "memory");
+}
+template <>
+__device__ inline void xload<5>(u32x4 (&w)[5], const u32x4 *const (&p)[5]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %5, off sc1\n\t"
+      "global_load_dwordx4 %1, %6, off sc1\n\t"
+      "global_load_dwordx4 %2, %7, off sc1\n\t"
+      "global_load_dwordx4 %3, %8, off sc1\n\t"
+      "global_load_dwordx4 %4, %9, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4])
+      : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4])
+      : "memory");
+}
+
+// Pollers: wait until the nw words at addr(0..nw-1) carry epoch ep, then hand each to
+// put(i, word).  K words per poller lane per pass; a lane past nw re-reads a word in range
+// and ignores it.  False on timeout or when another block raised the error word.
+template <int K, class Addr, class Put>
+__device__ __forceinline__ bool poll_k(int nw, uint32_t ep, uint32_t *err, int t, Addr addr, Put put) {
+  for (int base = 0; base < nw; base += K * kPollThreads) {
+    const u32x4 *p[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+      const int i = base + t + k * kPollThreads;
+      p[k] = addr(i < nw ? i : base);
+    }
+    u32x4 w[K];
+    long spins = 0;
+    while (true) {
+      xload<K>(w, p);
+      bool all = true;
+#pragma unroll
+      for (int k = 0; k < K; k++) all = all && (base + t + k * kPollThreads >= nw || w[k].w == ep);
+      if (__all(all)) break;
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+      if ((spins & 63) == 0 && ld_u32(err) != 0) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+      const int i = base + t + k * kPollThreads;
+      if (i < nw) put(i, w[k]);
+    }
+  }
+  return true;
+}
+
+template <class Addr, class Put>
+__device__ __forceinline__ bool poll(int nw, uint32_t ep, uint32_t *err, int t, Addr addr, Put put) {
+  if (nw <= kPollThreads) return poll_k<1>(nw, ep, err, t, addr, put);
+  if (nw <= 2 * kPollThreads) return poll_k<2>(nw, ep, err, t, addr, put);
+  return poll_k<5>(nw, ep, err, t, addr, put);
+}
+
+// Word j of a segment holding len values (starting at value 0) scattered to dst.
+__device__ inline void put_word(float *dst, int j, int len, u32x4 v) {
+  const int e0 = 3 * j;
+  if (e0 < len) dst[e0] = __uint_as_float(v.x);
+  if (e0 + 1 < len) dst[e0 + 1] = __uint_as_float(v.y);
+  if (e0 + 2 < len) dst[e0 + 2] = __uint_as_float(v.z);
+}
+
+// Pollers: the whole N-vector published by blocks (block s's rows as one segment of W
+// words) into dst[0..N); rs[s] = row_start(N, s, B) for s in [0, B] (LDS table).
+__device__ __forceinline__ bool poll_rows(const void *arr, int N, int B, const int *rs, uint32_t ep, float *dst,
+                                          uint32_t *err, int t) {
+  const int W = words_for((N + B - 1) / B);
+  const FastDiv divW(W);
+  const u32x4 *src = static_cast<const u32x4 *>(arr);
+  return poll(
+      B * W, ep, err, t, [&](int i) { return src + i; },
+      [&](int i, u32x4 v) {
+        const int s = divW(i), j = i - s * W;
+        const int r0 = rs[s];
+        put_word(dst + r0, j, rs[s + 1] - r0, v);
+      });
+}
+
+// Publisher lane j < W: the block's rows (vals[0..rows)) as its segment of arr.
+__device__ inline void publish_rows(void *arr, int N, int B, int b, const float *vals, int rows, uint32_t ep,
+                                    int lane) {
+  const int W = words_for((N + B - 1) / B);
+  if (lane < W) {
+    const int e0 = 3 * lane;
+    xstore(static_cast<u32x4 *>(arr) + b * W + lane, e0 < rows ? vals[e0] : 0.0f, e0 + 1 < rows ? vals[e0 + 1] : 0.0f,
+           e0 + 2 < rows ? vals[e0 + 2] : 0.0f, ep);
+  }
+}
+
+// ---- weights -----------------------------------------------------------------------
 // (scale, bias) of one group as held in registers: fp16x2 in one register, or float2.
 template <int PT>
 struct ParamReg {
@@ -221,9 +260,10 @@ __device__ inline void load_slots(Slots<PT, NS> &s, const DevQL &ql, const RowMa
   }
 }
 
-__device__ inline float dot16(const u32x4 c, const float *xc) {
+// 16 codes against 16 activations: (sum of code*x, sum of x).
+__device__ inline float2 dot16(const u32x4 c, const float *xc) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-  float acc = 0.0f;
+  float acc = 0.0f, xs = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const float4 xv = *reinterpret_cast<const float4 *>(xc + 4 * i);
@@ -231,14 +271,15 @@ __device__ inline float dot16(const u32x4 c, const float *xc) {
     acc += xv.y * (float)((w[i] >> 8) & 0xffu);
     acc += xv.z * (float)((w[i] >> 16) & 0xffu);
     acc += xv.w * (float)(w[i] >> 24);
+    xs += (xv.x + xv.y) + (xv.z + xv.w);
   }
-  return acc;
+  return make_float2(acc, xs);
 }
 
-// Loaders: per-chunk partial products into part[] (LDS).
+// Loaders: per-chunk partial products into part[] (LDS): scale * sum(code*x) + bias *
+// sum(x), the group affine folded per 16-value chunk.
 template <int PT, int NS>
-__device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const float *xn, const float *xsum,
-                                 float *part, int ll) {
+__device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const float *xn, float *part, int ll) {
   const int total = m.rows * m.C;
   // per-slot chunk indices are recomputed per call rather than hoisted out of the layer
   // loop (they would hold a register per slot and matrix for the whole step)
@@ -250,18 +291,64 @@ __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const 
     if (c < total) {
       const int kc = c % m.C;
       const float2 p = param_value(s.p[j]);
-      part[c] = p.x * dot16(s.c[j], xn + kc * 16) + p.y * xsum[kc];
+      const float2 r = dot16(s.c[j], xn + kc * 16);
+      part[c] = p.x * r.x + p.y * r.y;
     }
     // one chunk's activations in registers at a time
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// Loader waves sum the rows of part[] (a row is m.C chunk partials): 16 lanes per row,
-// four rows per wave, rows lw*4.. of each pass of 9 waves; in a fixed order.  The last
-// lane of a row receives the row value plus its bias (LDS) and calls epi(row, value).
+// ---- cross-lane reductions ---------------------------------------------------------------
+// DPP (ALU row shifts and broadcasts, no LDS round trip).  They need every lane of the wave
+// active.  Fixed order, so every block reduces identically.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ inline float dpp_f(float v, float old) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+// Inclusive scan within each row of 16 lanes: lane 15 of a row holds the row's sum.
+__device__ inline float row16_sum(float x) {
+  x += dpp_f<0x111, 0xf, 0xf>(x, 0.0f);  // row_shr:1
+  x += dpp_f<0x112, 0xf, 0xf>(x, 0.0f);  // row_shr:2
+  x += dpp_f<0x114, 0xf, 0xe>(x, 0.0f);  // row_shr:4, lanes 4-15
+  x += dpp_f<0x118, 0xf, 0xc>(x, 0.0f);  // row_shr:8, lanes 8-15
+  return x;
+}
+// Sum over the wave, returned to every lane.
+__device__ inline float wave64_sum(float x) {
+  x = row16_sum(x);
+  x += dpp_f<0x142, 0xa, 0xf>(x, 0.0f);  // row_bcast:15 into rows 1, 3
+  x += dpp_f<0x143, 0xc, 0xf>(x, 0.0f);  // row_bcast:31 into rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+// Max over the wave, returned to every lane.
+__device__ inline float wave64_max(float x) {
+  const float ni = -INFINITY;
+  x = fmaxf(x, dpp_f<0x111, 0xf, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x112, 0xf, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x114, 0xf, 0xe>(x, ni));
+  x = fmaxf(x, dpp_f<0x118, 0xf, 0xc>(x, ni));
+  x = fmaxf(x, dpp_f<0x142, 0xa, 0xf>(x, ni));
+  x = fmaxf(x, dpp_f<0x143, 0xc, 0xf>(x, ni));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// Loader waves sum the rows of part[] (a row is m.C chunk partials), in a fixed order:
+// rows of 256 chunks or more take a wave each (lane 0 calls epi), shorter rows 16 lanes
+// each, four rows per wave, rows lw*4.. of each pass of 9 waves (the last lane of a row
+// calls epi).  epi(row, value) receives the row value plus its bias (LDS).
 template <class Epi>
 __device__ inline void row_sums(const RowMap &m, const float *part, const float *bias, int lw, int lane, Epi epi) {
+  if (m.C >= 256) {  // long rows: a wave per row
+    for (int r = lw; r < m.rows; r += kLoadWaves) {
+      float acc = 0.0f;
+      for (int c = lane; c < m.C; c += 64) acc += part[r * m.C + c];
+      acc = wave64_sum(acc);
+      if (lane == 0) epi(r, acc + bias[r]);
+    }
+    return;
+  }
   const int sub = lane >> 4, sl = lane & 15;
   for (int r0 = lw * 4; r0 < m.rows; r0 += kLoadWaves * 4) {
     const int r = r0 + sub;
@@ -273,6 +360,7 @@ __device__ inline void row_sums(const RowMap &m, const float *part, const float 
   }
 }
 
+// ---- parameters -----------------------------------------------------------------------
 // Stages the LayerNorm parameters (4 x d) and the block's bias rows of layer l (or, for
 // l == n_layer, of the head) into one parameter buffer with LDS-DMA copies issued by one
 // wave (lane in [0, 64)): no registers are written, and nothing waits for the copies until
@@ -320,10 +408,9 @@ __device__ inline float bsum(float v, float *red, int tid) {
 }
 
 // LayerNorm (biased variance, eps 1e-5) of the LDS row x into the LDS row y (y may be x),
-// w and b in LDS, fused with the 16-element chunk sums of y that the GEMV consumes.
-// red holds 32 floats (two reductions' scratch).
-__device__ __forceinline__ void ln_chunks(const float *x, float *y, const float *w, const float *b, int n, float *xsum,
-                                 float *red, int tid) {
+// w and b in LDS.  red holds 32 floats (two reductions' scratch).
+__device__ __forceinline__ void layer_norm(const float *x, float *y, const float *w, const float *b, int n, float *red,
+                                           int tid) {
   float s = 0.0f;
   for (int i = tid; i < n; i += kThreads) s += x[i];
   const float mean = bsum(s, red, tid) / (float)n;
@@ -334,14 +421,7 @@ __device__ __forceinline__ void ln_chunks(const float *x, float *y, const float 
   }
   const float var = bsum(q, red + 16, tid) / (float)n;
   const float rstd = 1.0f / sqrtf(var + 1e-5f);
-  for (int base = 0; base < n; base += kThreads) {
-    const int i = base + tid;
-    const float v = i < n ? (x[i] - mean) * rstd * w[i] + b[i] : 0.0f;
-    if (i < n) y[i] = v;
-    // 16 consecutive threads hold one chunk
-    const float c = row16_sum(v);
-    if ((tid & 15) == 15 && i < n) xsum[i >> 4] = c;
-  }
+  for (int i = tid; i < n; i += kThreads) y[i] = (x[i] - mean) * rstd * w[i] + b[i];
   __syncthreads();
 }
 
@@ -363,7 +443,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   constexpr bool poller = ROLE == kRolePoll, pub = ROLE == kRolePub, loader = ROLE == kRoleLoad;
   DecodeCtl *ctl = a.ctl;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int ll = tid - kLoadWave0 * 64;                                  // loader lane
+  const int ll = tid - kLoadWave0 * 64;                                   // loader lane
   const int lw = __builtin_amdgcn_readfirstlane((tid >> 6) - kLoadWave0);  // loader wave
   const int B = gridDim.x, b = blockIdx.x;
   const int d = a.d, F = a.F, H = a.H, S = a.S;
@@ -372,14 +452,15 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   const uint32_t ep0 = xstep * a.ep_stride + 1u;
   const int L = vlen + 1;  // keys including the row this step appends
   uint32_t *err = a.err;
+  u32x4 *x_part = static_cast<u32x4 *>(a.x_part);
+  u32x4 *x_attn = static_cast<u32x4 *>(a.x_attn);
 
-  // LDS (floats): xin[xin_len] | xn[d] | xsum[xin_len/16] | part[part_len] | own[own_len] |
-  // own_mid[own_len] | out[out_len] | qs[64] | kn[64] | vn[64] | pp[S*66] |
-  // lp[2][lp_len] | kvs[2*3*576*4]; the host rounds every length to a multiple of 4
+  // LDS (floats): xin[xin_len] | xn[d] | part[part_len] | own[own_len] | own_mid[own_len] |
+  // out[out_len] | qs[64] | kn[64] | vn[64] | pp[S*66] | lp[2][lp_len] | kvs[2*3*576*4] |
+  // rs[3][B+1] (int); the host rounds every length to a multiple of 4
   float *xin = lds;
   float *xn = xin + a.xin_len;
-  float *xsum = xn + d;
-  float *part = xsum + a.xin_len / 16;
+  float *part = xn + d;
   float *own = part + a.part_len;
   float *own_mid = own + a.own_len;
   float *out = own_mid + a.own_len;
@@ -389,6 +470,10 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   float *pp = vn + 64;
   float *lpb = pp + a.pp_len;
   float *kvs = lpb + 2 * a.lp_len;  // [2][kKeyPasses][576] x 16 bytes
+  // row_start tables of the by-block exchange arrays: N = d, 3d, F; B + 1 entries each
+  int *rs_d = reinterpret_cast<int *>(kvs + 2 * kKeyPasses * kLoadThreads * 4);
+  int *rs_3d = rs_d + (B + 1);
+  int *rs_f = rs_3d + (B + 1);
 
   const RowMap m_qkv = rows_of(3 * d, d / 16, b, B);
   const RowMap m_proj = rows_of(d, d / 16, b, B);
@@ -418,6 +503,11 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     stage_params_dma(a, 0, lpb, m_qkv, m_proj, m_fc, m_mp, m_head, lane);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  for (int s2 = tid; s2 <= B; s2 += kThreads) {
+    rs_d[s2] = row_start(d, s2, B);
+    rs_3d[s2] = row_start(3 * d, s2, B);
+    rs_f[s2] = row_start(F, s2, B);
+  }
   __syncthreads();
   if (pub)
     for (int r = lane; r < m_proj.rows; r += 64) own[r] = xin[m_proj.row0 + r];
@@ -434,25 +524,24 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     const float *lp = lpb + (l & 1) * a.lp_len;
     // ---------------- P1: LN1, QKV rows; K/V rows into the cache --------------------
     if (l > 0) {
-      if (poller && !poll_words<kPollD>(a.x_x, d, ep - 8u + 6u, xin, err, T)) sh.abort = 1;
+      if (poller && !poll_rows(a.x_x, d, B, rs_d, ep - 8u + 6u, xin, err, T)) sh.abort = 1;
       __syncthreads();
       if (sh.abort) return;
     }
-    ln_chunks(xin, xn, lp, lp + d, d, xsum, sh.red, T);
-    if (loader) dot_slots(wq, m_qkv, xn, xsum, part, ll);
+    layer_norm(xin, xn, lp, lp + d, d, sh.red, T);
+    if (loader) dot_slots(wq, m_qkv, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_qkv, part, lp + bo_q, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
     if (pub) {
+      publish_rows(a.x_qkv, 3 * d, B, b, out, m_qkv.rows, ep + 1u, lane);
       for (int r = lane; r < m_qkv.rows; r += 64) {
         const int R = m_qkv.row0 + r;
-        const float v = out[r];
-        ll_store(a.x_qkv + R, ep + 1u, v);
         if (R >= d) {
           const int idx = R < 2 * d ? R - d : R - 2 * d;
           const int h = idx >> 6, e = idx & 63;
           uint16_t *cache = static_cast<uint16_t *>(R < 2 * d ? a.kc : a.vc);
-          cache[(((size_t)l * H + h) * a.max_seq + vlen) * 64 + e] = (uint16_t)float_to_bf16_bits(v);
+          cache[(((size_t)l * H + h) * a.max_seq + vlen) * 64 + e] = (uint16_t)float_to_bf16_bits(out[r]);
         }
       }
     }
@@ -484,11 +573,53 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
         }
       }
       if (poller) {
-        bool ok = poll_words<1>(a.x_qkv + ah * 64, 64, ep + 1u, qs, err, T);
-        if (ok && j1 == L) {  // this split holds the appended row
-          ok = poll_words<1>(a.x_qkv + d + ah * 64, 64, ep + 1u, kn, err, T) &&
-               poll_words<1>(a.x_qkv + 2 * d + ah * 64, 64, ep + 1u, vn, err, T);
-        }
+        // q (and, for the split holding the appended row, k and v) of head ah: the words
+        // of the blocks whose QKV rows cover them, polled together
+        const int N3 = 3 * d, Wq = words_for((N3 + B - 1) / B);
+        const int *rs3 = rs_3d;
+        const bool kv_too = j1 == L;
+        const int lq = ah * 64, lk = d + ah * 64, lv = 2 * d + ah * 64;
+        const int bq = block_of(N3, lq, B), bk = block_of(N3, lk, B), bv = block_of(N3, lv, B);
+        const int nq = (block_of(N3, lq + 63, B) - bq + 1) * Wq;
+        const int nk = kv_too ? (block_of(N3, lk + 63, B) - bk + 1) * Wq : 0;
+        const int nv = kv_too ? (block_of(N3, lv + 63, B) - bv + 1) * Wq : 0;
+        const u32x4 *src = static_cast<const u32x4 *>(a.x_qkv);
+        const FastDiv divWq(Wq);
+        // word i of the concatenation (q words, then k, then v) -> its group's first block,
+        // first row and destination, and its index within the group
+        auto group = [&](int i, int &gb, int &lo, float *&dst) {
+          if (i < nq) {
+            gb = bq, lo = lq, dst = qs;
+            return i;
+          }
+          if (i < nq + nk) {
+            gb = bk, lo = lk, dst = kn;
+            return i - nq;
+          }
+          gb = bv, lo = lv, dst = vn;
+          return i - nq - nk;
+        };
+        const bool ok = poll(
+            nq + nk + nv, ep + 1u, err, T,
+            [&](int i) {
+              int gb, lo;
+              float *dst;
+              const int li = group(i, gb, lo, dst);
+              return src + gb * Wq + li;
+            },
+            [&](int i, u32x4 v) {
+              int gb, lo;
+              float *dst;
+              const int li = group(i, gb, lo, dst);
+              const int sq = divWq(li), s = gb + sq, j = li - sq * Wq;
+              const int r0 = rs3[s], len = rs3[s + 1] - r0;
+              const float f[3] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z)};
+#pragma unroll
+              for (int e = 0; e < 3; e++) {
+                const int rr = r0 + 3 * j + e;
+                if (3 * j + e < len && rr >= lo && rr < lo + 64) dst[rr - lo] = f[e];
+              }
+            });
         if (!ok) sh.abort = 1;
       }
       __syncthreads();
@@ -582,13 +713,19 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       if (pub) {
         float osum = 0.0f;
         for (int w = 0; w < kLoadWaves * 4; w++) osum += kvs[w * 64 + lane];
-        uint64_t *pw = a.x_part + ((size_t)ah * S + aj) * 66;
-        ll_store(pw + 2 + lane, ep + 2u, osum);
+        float lt = 0.0f;
+        for (int w = 0; w < kLoadWaves; w++) lt += sh.l_w[w];
+        // [M, l, o0..o63] staged in qs (free after the scores) for the word layout
+        qs[2 + lane] = osum;
         if (lane == 0) {
-          float lt = 0.0f;
-          for (int w = 0; w < kLoadWaves; w++) lt += sh.l_w[w];
-          ll_store(pw, ep + 2u, M);
-          ll_store(pw + 1, ep + 2u, lt);
+          qs[0] = M;
+          qs[1] = lt;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane < kPartWords) {
+          const int e0 = 3 * lane;
+          xstore(x_part + (ah * S + aj) * kPartWords + lane, qs[e0], e0 + 1 < kPartVals ? qs[e0 + 1] : 0.0f,
+                 e0 + 2 < kPartVals ? qs[e0 + 2] : 0.0f, ep + 2u);
         }
       }
       if (poller && T == 0) {
@@ -598,28 +735,47 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       }
       __syncthreads();
       if (sh.last) {
-        if (poller && !poll_words<2>(a.x_part + (size_t)ah * S * 66, S * 66, ep + 2u, pp, err, T)) sh.abort = 1;
+        if (poller && !poll(
+                          S * kPartWords, ep + 2u, err, T,
+                          [&](int i) { return x_part + ah * S * kPartWords + i; },
+                          [&](int i, u32x4 v) {
+                            const int s = i / kPartWords;
+                            put_word(pp + s * kPartVals, i - s * kPartWords, kPartVals, v);
+                          }))
+          sh.abort = 1;
         __syncthreads();
         if (sh.abort) return;
         if (pub) {
           float Mg = -INFINITY;
-          for (int s = 0; s < S; s++) Mg = fmaxf(Mg, pp[s * 66]);
+          for (int s = 0; s < S; s++) Mg = fmaxf(Mg, pp[s * kPartVals]);
           float den = 0.0f, num = 0.0f;
           for (int s = 0; s < S; s++) {
-            if (pp[s * 66] == -INFINITY) continue;
-            const float f = __expf(pp[s * 66] - Mg);
-            den += pp[s * 66 + 1] * f;
-            num += pp[s * 66 + 2 + lane] * f;
+            if (pp[s * kPartVals] == -INFINITY) continue;
+            const float f = __expf(pp[s * kPartVals] - Mg);
+            den += pp[s * kPartVals + 1] * f;
+            num += pp[s * kPartVals + 2 + lane] * f;
           }
-          ll_store(a.x_attn + ah * 64 + lane, ep + 3u, num / den);
+          qs[lane] = num / den;  // staged for the word layout
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane < kHeadWords) {
+            const int e0 = 3 * lane;
+            xstore(x_attn + ah * kHeadWords + lane, qs[e0], e0 + 1 < 64 ? qs[e0 + 1] : 0.0f,
+                   e0 + 2 < 64 ? qs[e0 + 2] : 0.0f, ep + 3u);
+          }
         }
       }
     }
     // ---------------- P3: c_proj rows + residual ------------------------------------
-    if (poller && !poll_words<kPollD>(a.x_attn, d, ep + 3u, xin, err, T, xsum)) sh.abort = 1;
+    if (poller && !poll(
+                      H * kHeadWords, ep + 3u, err, T, [&](int i) { return x_attn + i; },
+                      [&](int i, u32x4 v) {
+                        const int h = i / kHeadWords;
+                        put_word(xin + h * 64, i - h * kHeadWords, 64, v);
+                      }))
+      sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    if (loader) dot_slots(wp, m_proj, xin, xsum, part, ll);
+    if (loader) dot_slots(wp, m_proj, xin, part, ll);
     __syncthreads();
     if (loader)
       row_sums(m_proj, part, lp + bo_p, lw, lane, [&](int r, float v) {
@@ -628,30 +784,29 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
         out[r] = xm;
       });
     __syncthreads();
-    if (pub)
-      for (int r = lane; r < m_proj.rows; r += 64) ll_store(a.x_mid + m_proj.row0 + r, ep + 4u, out[r]);
+    if (pub) publish_rows(a.x_mid, d, B, b, out, m_proj.rows, ep + 4u, lane);
     // prefetches are issued once the phase's outputs are out (issuing them earlier delays
     // the row sums behind the memory pipeline)
     if (loader) load_slots<PT>(wm, Ly.mproj, m_mp, ll);
     // ---------------- P4: LN2, c_fc rows + GELU ------------------------------------
-    if (poller && !poll_words<kPollD>(a.x_mid, d, ep + 4u, xin, err, T)) sh.abort = 1;
+    if (poller && !poll_rows(a.x_mid, d, B, rs_d, ep + 4u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    ln_chunks(xin, xn, lp + 2 * d, lp + 3 * d, d, xsum, sh.red, T);
-    if (loader) dot_slots(wf, m_fc, xn, xsum, part, ll);
+    layer_norm(xin, xn, lp + 2 * d, lp + 3 * d, d, sh.red, T);
+    if (loader) dot_slots(wf, m_fc, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_fc, part, lp + bo_f, lw, lane, [&](int r, float v) { out[r] = gelu_tanh(v); });
     __syncthreads();
     if (pub) {
-      for (int r = lane; r < m_fc.rows; r += 64) ll_store(a.x_f + m_fc.row0 + r, ep + 5u, out[r]);
+      publish_rows(a.x_f, F, B, b, out, m_fc.rows, ep + 5u, lane);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next layer's parameter copies
     }
     if (loader && l + 1 < a.n_layer) load_slots<PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
     // ---------------- P5: mlp c_proj rows + residual ---------------------------------
-    if (poller && !poll_words<kPollF>(a.x_f, F, ep + 5u, xin, err, T, xsum)) sh.abort = 1;
+    if (poller && !poll_rows(a.x_f, F, B, rs_f, ep + 5u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    if (loader) dot_slots(wm, m_mp, xin, xsum, part, ll);
+    if (loader) dot_slots(wm, m_mp, xin, part, ll);
     __syncthreads();
     if (loader)
       row_sums(m_mp, part, lp + bo_m, lw, lane, [&](int r, float v) {
@@ -660,8 +815,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
         out[r] = xo;
       });
     __syncthreads();
-    if (pub)
-      for (int r = lane; r < m_mp.rows; r += 64) ll_store(a.x_x + m_mp.row0 + r, ep + 6u, out[r]);
+    if (pub) publish_rows(a.x_x, d, B, b, out, m_mp.rows, ep + 6u, lane);
     if (loader && l + 1 < a.n_layer) load_slots<PT>(wp, a.layers[l + 1].proj, m_proj, ll);
   }
   // ---------------- head: ln_f, final_norm, mel_head rows -> logits ------------------
@@ -670,12 +824,12 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (loader) load_slots<PT>(wh, a.head, m_head, ll);
     const uint32_t ep = ep0 + (uint32_t)(a.n_layer - 1) * 8u;
     const float *lp = lpb + (a.n_layer & 1) * a.lp_len;
-    if (poller && !poll_words<kPollD>(a.x_x, d, ep + 6u, xin, err, tid)) sh.abort = 1;
+    if (poller && !poll_rows(a.x_x, d, B, rs_d, ep + 6u, xin, err, tid)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    ln_chunks(xin, xn, lp, lp + d, d, xsum, sh.red, tid);
-    ln_chunks(xn, xn, lp + 2 * d, lp + 3 * d, d, xsum, sh.red, tid);
-    if (loader) dot_slots(wh, m_head, xn, xsum, part, ll);
+    layer_norm(xin, xn, lp, lp + d, d, sh.red, tid);
+    layer_norm(xn, xn, lp + 2 * d, lp + 3 * d, d, sh.red, tid);
+    if (loader) dot_slots(wh, m_head, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_head, part, lp + 4 * d, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
@@ -717,6 +871,8 @@ bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int
   const int S = std::min(12, B / H);
   if (S < 1) return false;
   if ((max_seq + S - 1) / S > kKeySlots * kKeyPasses) return false;
+  // one publisher wave writes a block's words of any array
+  if ((3 * d + B - 1) / B > 3 * 64 || (F + B - 1) / B > 3 * 64) return false;
   auto fits = [&](int N, int C, int slots) {
     return (long)((N + B - 1) / B) * C <= (long)slots * kLoadThreads;
   };
@@ -727,9 +883,20 @@ bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int
   return true;
 }
 
+size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]) {
+  auto w = [&](int N) { return (size_t)B * (((N + B - 1) / B + 2) / 3); };
+  const size_t n[6] = {w(d), w(3 * d), (size_t)H * S * kPartWords, (size_t)H * kHeadWords, w(d), w(F)};
+  size_t t = 0;
+  for (int i = 0; i < 6; i++) {
+    off[i] = t;
+    t += n[i];
+  }
+  return t;
+}
+
 size_t persist_lds_bytes(const PersistArgs &a) {
-  const size_t f = (size_t)a.xin_len + a.d + a.xin_len / 16 + a.part_len + 2 * (size_t)a.own_len + a.out_len +
-                   3 * 64 + a.pp_len + 2 * (size_t)a.lp_len + 2 * kKeyPasses * kLoadThreads * 4;
+  const size_t f = (size_t)a.xin_len + a.d + a.part_len + 2 * (size_t)a.own_len + a.out_len + 3 * 64 + a.pp_len +
+                   2 * (size_t)a.lp_len + 2 * kKeyPasses * kLoadThreads * 4 + 3 * (size_t)(a.B + 1);
   return f * sizeof(float);
 }
 

@@ -478,22 +478,20 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
                      "max_seq %d, %d compute units)",
                      kv->max_seq, B);
   if (!ok || g->path == ITTS_DECODE_MULTI) return ITTS_OK;
-  // exchange arrays, each followed by kPersistPad readable words
-  const size_t P = kPersistPad;
-  const size_t n_x = d + P, n_qkv = 3 * (size_t)d + P, n_part = (size_t)H * S * 66 + P, n_f = F + P;
-  const size_t words = n_x + n_qkv + n_part + n_x + n_x + n_f;
+  size_t off[6];
+  const size_t words = persist_exchange_words(d, F, H, S, B, off);
   const size_t sync_words = (size_t)H * kCntStride + 64;
-  HIP_TRY(kv->xch.ensure(words * sizeof(uint64_t)));
+  HIP_TRY(kv->xch.ensure(words * 16));
   HIP_TRY(kv->sync.ensure(sync_words * sizeof(uint32_t)));
   HIP_TRY(hipMemsetAsync(kv->xch.p, 0, kv->xch.bytes, g->stream));
   HIP_TRY(hipMemsetAsync(kv->sync.p, 0, kv->sync.bytes, g->stream));
-  uint64_t *x = kv->xch.as<uint64_t>();
-  a.x_x = x;
-  a.x_qkv = a.x_x + n_x;
-  a.x_part = a.x_qkv + n_qkv;
-  a.x_attn = a.x_part + n_part;
-  a.x_mid = a.x_attn + n_x;
-  a.x_f = a.x_mid + n_x;
+  char *x = static_cast<char *>(kv->xch.p);
+  a.x_x = x + off[0] * 16;
+  a.x_qkv = x + off[1] * 16;
+  a.x_part = x + off[2] * 16;
+  a.x_attn = x + off[3] * 16;
+  a.x_mid = x + off[4] * 16;
+  a.x_f = x + off[5] * 16;
   a.cnt = kv->sync.as<uint32_t>();
   a.err = a.cnt + (size_t)H * kCntStride;
   a.layers = g->dlayers.as<DevLayer>();
