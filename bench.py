@@ -97,6 +97,19 @@ def cpu_baseline(W, prompt, sp, n_steps: int):
     }
 
 
+def measured_traffic(decode_path):
+    """HBM bytes per launch of the persistent step from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
+    if decode_path != "persistent":
+        return None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_persist_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,7 +194,15 @@ def main():
     step_ms = dec_ms / dec_steps
     mean_L = T + (dec_steps + 1) / 2.0  # keys of step i: T + i + 1, i = 0..dec_steps-1
     bytes_step = step_bytes(weight_bytes, int(round(mean_L)))
-    achieved = bytes_step / (step_ms * 1e-3) / 1e9
+
+    # The dominant kernel alone: the same decode steps (contexts T+1 .. T+dec_steps, so the
+    # same mean context) launched back to back between HIP events on the decoder's stream.
+    g.prefill(prompt.text_tokens, prompt.conds, prompt.lang_id, kv, logits=False)
+    kernel_ms = kv.decode_timing(100, 2, dec_steps)
+    achieved = bytes_step / (kernel_ms * 1e-3) / 1e9
+    kernel_name = ("decode_persist_kernel (one launch = one decode step)" if decode_path == "persistent"
+                   else "decode step (122 kernels)")
+    traffic = measured_traffic(decode_path)
     value = args.steps * n_tok / wall
     out = {
         "metric": METRIC,
@@ -205,10 +226,10 @@ def main():
         "decode_step_us": round(step_ms * 1e3, 2),
         "prefill_ms": round(pre_ms, 3),
         "gpu_region_ms": round(region_ms.value, 3),
+        "decode_kernel_us": round(kernel_ms * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "decode step (one replay of the sample+step graph)",
+                     "traffic": traffic, "kernel": kernel_name,
                      "bytes_per_launch": bytes_step, "mean_keys": mean_L},
     }
     if not args.no_cpu_baseline:

@@ -233,6 +233,13 @@ itts_status itts_dequantize(itts_gpt *gpt, const itts_qlinear *ql, int32_t N, in
 itts_status itts_qlinear_forward(itts_gpt *gpt, const itts_qlinear *ql, int32_t N, int32_t K,
                                  int32_t bits, itts_dtype param_dtype, const float *x,
                                  int32_t M, float *y);
+/* Times the decode step alone: n_steps steps, each of mel_token_id at position pos_idx,
+ * enqueued back to back on the decoder's stream after the cache's valid_len rows and
+ * bracketed by HIP events; *ms_per_step = elapsed / n_steps.  The cache grows by n_steps
+ * rows (the last step's logits stay on the device).  No counterpart in the reference: a
+ * measurement helper for the step kernel(s). */
+itts_status itts_decode_timing(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int32_t pos_idx,
+                               int32_t n_steps, float *ms_per_step);
 
 #ifdef __cplusplus
 }

@@ -119,8 +119,9 @@ size_t persist_lds_bytes(const PersistArgs &a);
 // 16-byte words of the exchange arrays x_x, x_qkv, x_part, x_attn, x_mid, x_f: total, and
 // each array's offset in off[6].
 size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]);
-// Blocks of the persistent kernel that fit on one compute unit with `lds` bytes of LDS.
-hipError_t persist_blocks_per_cu(int ptype, size_t lds, int *blocks);
+// Whether one block of the persistent kernel with `lds` bytes of dynamic LDS fits a
+// compute unit (threads, static + dynamic LDS).
+hipError_t persist_fits(int ptype, size_t lds, bool *fits);
 hipError_t launch_decode_persist(PersistArgs a, int ptype, hipStream_t s);
 // Raises the kernel's dynamic-LDS limit; once per process, outside stream capture.
 hipError_t persist_init();

@@ -917,10 +917,21 @@ hipError_t persist_init() {
   return hipSuccess;
 }
 
-hipError_t persist_blocks_per_cu(int ptype, size_t lds, int *blocks) {
+hipError_t persist_fits(int ptype, size_t lds, bool *fits) {
   const void *fn = ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<kParamF16>)
                                       : reinterpret_cast<const void *>(decode_persist_kernel<kParamF32>);
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks, fn, kThreads, lds);
+  hipFuncAttributes fa{};
+  hipError_t e = hipFuncGetAttributes(&fa, fn);
+  if (e != hipSuccess) return e;
+  int dev = 0, max_lds = 0;
+  if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+  if ((e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev)) != hipSuccess)
+    return e;
+  // 1024 threads use the whole CU (16 waves); the compiler bounded the registers for that
+  // (launch bounds), so the block fits when its LDS does
+  *fits = fa.maxThreadsPerBlock >= kThreads && fa.sharedSizeBytes + lds <= (size_t)max_lds &&
+          lds <= kPersistMaxLds;
+  return hipSuccess;
 }
 
 }  // namespace itts

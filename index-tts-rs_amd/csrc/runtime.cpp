@@ -467,11 +467,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     a.lp_len = r4(4 * d + std::max(rq + rp + rf + rp, rh));
   }
   bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
-  if (ok) {
-    int per_cu = 0;
-    HIP_TRY(persist_blocks_per_cu(g->ptype(), persist_lds_bytes(a), &per_cu));
-    ok = per_cu >= 1;  // one block per compute unit, all co-resident
-  }
+  if (ok) HIP_TRY(persist_fits(g->ptype(), persist_lds_bytes(a), &ok));  // one block per CU
   if (g->path == ITTS_DECODE_PERSISTENT && !ok)
     return set_error(ITTS_E_VALIDATION,
                      "decode_path: the persistent decode step does not support this cache (bf16 rows, "
@@ -1038,6 +1034,39 @@ itts_status itts_generate_codes(itts_gpt *gpt, itts_kv *kv, const int32_t *text_
   pr.n_cond = n_cond;
   pr.lang_id = lang_id;
   return itts_generate_codes_after(gpt, kv, &pr, p, rng_state, codes_out, codes_cap, n_codes);
+}
+
+itts_status itts_decode_timing(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int32_t pos_idx, int32_t n_steps,
+                               float *ms_per_step) {
+  if (!gpt || !kv || !ms_per_step || kv->gpt != gpt) return set_error(ITTS_E_VALIDATION, "timing: bad argument");
+  const itts_config &c = gpt->cfg;
+  if (n_steps < 1) return set_error(ITTS_E_VALIDATION, "n_steps: must be >= 1");
+  if (mel_token_id < 0 || mel_token_id >= c.mel_vocab)
+    return set_error(ITTS_E_VALIDATION, "mel_token_id: mel_token_id %d out of range 0..%d", mel_token_id,
+                     c.mel_vocab);
+  if (pos_idx < 0 || pos_idx >= c.mel_pos_len)
+    return set_error(ITTS_E_VALIDATION, "pos_idx: pos_idx %d out of range 0..%d", pos_idx, c.mel_pos_len);
+  if (kv->valid_len + n_steps > kv->max_seq)
+    return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
+                     kv->valid_len + n_steps, kv->max_seq);
+  for (hipEvent_t &ev : kv->ev_t)
+    if (!ev) HIP_TRY(hipEventCreate(&ev));
+  DecodeCtl h{};
+  h.tok = mel_token_id;
+  h.pos = pos_idx;
+  h.valid_len = kv->valid_len;
+  if (itts_status st = write_ctl(kv, h)) return st;
+  HIP_TRY(hipEventRecord(kv->ev_t[0], gpt->stream));
+  for (int i = 0; i < n_steps; i++)
+    if (itts_status st = enqueue_decode_step(gpt, kv)) return st;
+  HIP_TRY(hipEventRecord(kv->ev_t[1], gpt->stream));
+  HIP_TRY(hipEventSynchronize(kv->ev_t[1]));
+  if (itts_status st = check_persist(kv)) return st;
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, kv->ev_t[0], kv->ev_t[1]));
+  kv->valid_len += n_steps;
+  *ms_per_step = ms / (float)n_steps;
+  return ITTS_OK;
 }
 
 // ---- quantiser ----

@@ -155,6 +155,8 @@ _SIGS = {
                                   C.c_int32, C.c_int, C.c_void_p]),
     "itts_qlinear_forward": (C.c_int, [C.c_void_p, C.POINTER(itts_qlinear), C.c_int32, C.c_int32,
                                        C.c_int32, C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
+    "itts_decode_timing": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                     C.POINTER(C.c_float)]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
@@ -358,6 +360,13 @@ class KvCache:
         t = itts_timing()
         _check(lib.itts_kv_last_timing(self._h, C.byref(t)))
         return {f: getattr(t, f) for f, _ in itts_timing._fields_}
+
+    def decode_timing(self, mel_token_id: int, pos_idx: int, n_steps: int) -> float:
+        """Milliseconds per decode step over n_steps back-to-back steps (the cache grows)."""
+        ms = C.c_float()
+        _check(lib.itts_decode_timing(self.gpt._h, self._h, int(mel_token_id), int(pos_idx), int(n_steps),
+                                      C.byref(ms)))
+        return ms.value
 
     def read(self, layer: int, which_v: bool) -> np.ndarray:
         cfg = self.gpt.cfg
