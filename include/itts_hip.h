@@ -133,10 +133,18 @@ itts_status itts_sampling_validate(const itts_sampling *p);
 /* ---- Gpt (gpt.rs:438-525) ---- */
 /* Gpt::from_weights: validates the shape, uploads and repacks every tensor. */
 itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out);
+/* Gpt::load_from_path (gpt.rs:522) for gpt_int8.safetensors: the safetensors header is
+ * validated as loader.rs:1410-1458 does, every tensor is checked by name, shape and dtype
+ * as Gpt::from_weights does (gpt.rs:477-515, 269-323, 229-247), and the decoder shape is
+ * read from the file.  U32 codes are consumed as bytes; F32 (the shipped checkpoint) or
+ * F16 group parameters.  Errors: ITTS_E_WEIGHT "weight load error in `<tensor>`: ...". */
+itts_status itts_gpt_load_safetensors(const char *path, itts_gpt **out);
 /* Releases the caller's handle.  Live KV caches keep the decoder's device state until
  * they are destroyed too, so the two may be destroyed in either order. */
 void itts_gpt_destroy(itts_gpt *gpt);
 int32_t itts_gpt_num_layers(const itts_gpt *gpt);        /* Gpt::num_layers */
+/* The decoder's shape (as created or read from the checkpoint). */
+itts_config itts_gpt_config(const itts_gpt *gpt);
 int32_t itts_gpt_max_cond(const itts_gpt *gpt);
 /* The HIP stream every kernel of this decoder runs on (hipStream_t). */
 void *itts_gpt_stream(const itts_gpt *gpt);

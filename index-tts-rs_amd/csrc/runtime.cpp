@@ -34,6 +34,18 @@ itts_status set_error(itts_status st, const char *fmt, ...) {
   return st;
 }
 
+}  // namespace
+
+// Error text from other translation units of the library (the safetensors loader).
+namespace itts {
+itts_status set_error_text(itts_status st, const char *msg) {
+  g_last_error = msg;
+  return st;
+}
+}  // namespace itts
+
+namespace {
+
 #define HIP_TRY(expr)                                                                    \
   do {                                                                                   \
     hipError_t e_ = (expr);                                                              \
@@ -671,6 +683,7 @@ void itts_gpt_destroy(itts_gpt *gpt) {
 }
 
 int32_t itts_gpt_num_layers(const itts_gpt *gpt) { return gpt ? gpt->cfg.n_layer : 0; }
+itts_config itts_gpt_config(const itts_gpt *gpt) { return gpt ? gpt->cfg : itts_config{}; }
 int32_t itts_gpt_max_cond(const itts_gpt *gpt) { return gpt ? gpt->max_cond : 0; }
 void *itts_gpt_stream(const itts_gpt *gpt) { return gpt ? (void *)gpt->stream : nullptr; }
 

@@ -117,7 +117,9 @@ _SIGS = {
     "itts_sampling_validate": (C.c_int, [C.POINTER(itts_sampling)]),
     "itts_gpt_create": (C.c_int, [C.POINTER(itts_weights), C.POINTER(C.c_void_p)]),
     "itts_gpt_destroy": (None, [C.c_void_p]),
+    "itts_gpt_load_safetensors": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
     "itts_gpt_num_layers": (C.c_int32, [C.c_void_p]),
+    "itts_gpt_config": (itts_config, [C.c_void_p]),
     "itts_gpt_max_cond": (C.c_int32, [C.c_void_p]),
     "itts_gpt_stream": (C.c_void_p, [C.c_void_p]),
     "itts_gpt_set_decode_path": (C.c_int, [C.c_void_p, C.c_int]),
@@ -189,6 +191,10 @@ def _ptr(a: np.ndarray | None):
 
 def version() -> str:
     return lib.itts_version().decode()
+
+
+def last_error() -> str:
+    return lib.itts_last_error().decode()
 
 
 # ----------------------------------------------------------------------------------
@@ -264,6 +270,18 @@ class Gpt:
         del keep  # the library has copied every tensor to the device
         self._h = h
         self.cfg = weights.cfg
+
+    @classmethod
+    def load_from_path(cls, path: str) -> "Gpt":
+        """Gpt::load_from_path: a gpt_int8 safetensors checkpoint."""
+        self = cls.__new__(cls)
+        self._weights = None
+        h = C.c_void_p()
+        _check(lib.itts_gpt_load_safetensors(os.fsencode(path), C.byref(h)))
+        self._h = h
+        c = lib.itts_gpt_config(h)
+        self.cfg = {n: getattr(c, n) for n, _ in itts_config._fields_}
+        return self
 
     def close(self):
         if getattr(self, "_h", None):

@@ -174,3 +174,47 @@ def make_prompt(cfg: dict, n_cond: int, n_text: int, seed: int = 0, lang_id: int
     conds = g.standard_normal((n_cond, cfg["d_model"]), dtype=np.float32)
     text = g.integers(2, cfg["text_vocab"], size=n_text, dtype=np.int64).astype(np.int32)
     return Prompt(text, conds, min(lang_id, cfg["lang_vocab"] - 1))
+
+
+def save_safetensors(W: ModelWeights, path: str, drop: tuple = (), override: dict | None = None) -> dict:
+    """Writes W as a gpt_int8 checkpoint in the reference's tensor layout
+    (crates/core/src/models/gpt.rs:477-515, 269-323, 229-247): F32 tables and LayerNorm
+    vectors, each QuantizedLinear as `weight` U32 [N][K*bits/32] (the code bytes in
+    little-endian words), `scales`/`biases` [N][K/64] (F32, or F16 for fp16 params) and
+    `bias` F32 [N].  `drop` omits tensors and `override` replaces them (error tests).
+    Returns the tensor dict written."""
+    from safetensors.numpy import save_file
+
+    t = {}
+
+    def params(a):
+        return a.view(np.float16) if a.dtype == np.uint16 else a.astype(np.float32)
+
+    def ql(prefix, q):
+        t[prefix + ".weight"] = np.ascontiguousarray(q.codes).view(np.uint32)
+        t[prefix + ".scales"] = params(q.scales)
+        t[prefix + ".biases"] = params(q.biases)
+        t[prefix + ".bias"] = q.bias.astype(np.float32)
+
+    t["text_embedding.weight"] = W.text_emb
+    t["lang_embedding.weight"] = W.lang_emb
+    t["mel_embedding.weight"] = W.mel_emb
+    t["mel_pos_embedding.emb.weight"] = W.mel_pos
+    t["text_pos_embedding.emb.weight"] = W.text_pos
+    for i, L in enumerate(W.layers):
+        p = f"gpt.h.{i}"
+        t[p + ".ln_1.weight"], t[p + ".ln_1.bias"] = L.ln1_w, L.ln1_b
+        t[p + ".ln_2.weight"], t[p + ".ln_2.bias"] = L.ln2_w, L.ln2_b
+        ql(p + ".attn.c_attn", L.c_attn)
+        ql(p + ".attn.c_proj", L.c_proj)
+        ql(p + ".mlp.c_fc", L.c_fc)
+        ql(p + ".mlp.c_proj", L.mlp_c_proj)
+    t["gpt.ln_f.weight"], t["gpt.ln_f.bias"] = W.ln_f_w, W.ln_f_b
+    t["final_norm.weight"], t["final_norm.bias"] = W.fn_w, W.fn_b
+    ql("mel_head", W.head)
+    for k in drop:
+        t.pop(k)
+    t.update(override or {})
+    t = {k: np.ascontiguousarray(v) for k, v in t.items()}
+    save_file(t, path, metadata={"format": "mlx"})
+    return t
