@@ -103,6 +103,16 @@ __device__ inline uint32_t float_to_bf16_bits(float f) {
   return x >> 16;
 }
 
+// x -> fp16 pair (hi, lo) with x = hi + lo to ~2^-22 relative (lo absorbs the rounding
+// of hi; values below the fp16 normal range keep an absolute error under 2^-25).  |x| is
+// clamped to the fp16 range for hi, so activations must stay below 65504 in magnitude.
+__device__ inline void split_f16(float x, uint32_t &hi, uint32_t &lo) {
+  const _Float16 h = (_Float16)fminf(fmaxf(x, -65504.0f), 65504.0f);
+  const _Float16 l = (_Float16)(x - (float)h);
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, l);
+}
+
 // (scale, bias) of one (row, group).
 template <int PT>
 __device__ inline float2 load_param(const void *params, size_t idx) {

@@ -22,6 +22,18 @@ struct AttnPartials {
 };
 enum Epilogue : int { kEpiStore = 0, kEpiResid = 1, kEpiGelu = 2, kEpiQKV = 3 };
 
+// Activations as the prefill GEMM reads them: x = hi + lo (fp16 planes, ~22 significant
+// bits) and the row sums of each 64-column group (the MLX bias term needs sum_k x).
+struct SplitAct {
+  const uint16_t *hi, *lo;  // [M][K]
+  const float *gs;          // [M][K/64]
+};
+struct SplitOut {
+  uint16_t *hi, *lo;
+  float *gs;
+  SplitAct act() const { return SplitAct{hi, lo, gs}; }
+};
+
 // Where the QKV epilogue scatters: q -> q_out[M][d]; k, v -> this layer's cache
 // [n_head][max_seq][64] at rows pos0.. (pos0 = ctl->valid_len when ctl != nullptr).
 struct QkvDst {
@@ -59,9 +71,10 @@ hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, in
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,
                               int kvt, hipStream_t s);
 
-// Causal attention of T rows at cache positions base..base+T-1 (prefill).
+// Causal attention of T rows at cache positions base..base+T-1 (prefill); the output
+// rows [T][d] are written in the GEMM's split form.
 hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
-                               int n_head, int max_seq, float *out, int kvt, hipStream_t s);
+                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s);
 
 // Row descriptors for the prefill embedding.
 struct EmbedRow {
@@ -74,19 +87,32 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
                              const float *text_pos, const float *mel_emb,
                              const float *mel_pos, int d, float *x, hipStream_t s);
 
-// LN of T rows [T][d] -> [T][d].
+// LN of T rows [T][d] -> [T][d] in the GEMM's split form.
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
-                          float *y, hipStream_t s);
+                          const SplitOut &y, hipStream_t s);
 
 // Prefill GEMM: y = x[M][K] . Wdeq^T + bias with the same epilogues as the GEMV.
 struct GemmArgs {
   DevQL ql;
-  const float *x;   // [M][K]
+  SplitAct x;       // [M][K]
   int M;
-  float *y;         // [M][N] (store / gelu) or residual stream [M][N] (resid)
+  float *y;         // [M][N] (store) or residual stream [M][N] (resid)
+  SplitOut xo;      // gelu: the next GEMM's input [M][N] (N a multiple of 64)
   QkvDst qkv;
+  // split-K partial tiles and per-tile arrival counters (zero between launches); split-K
+  // is not used when they are absent or too small
+  float *ws;
+  size_t ws_floats;
+  uint32_t *cnt;
+  int cnt_words;
+  int n_cu;         // compute units (grid sizing)
 };
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s);
+size_t gemm_ws_floats(int n_cu);
+constexpr int kGemmCounters = 4096;
+
+// fp32 rows [M][K] -> the GEMM's split form.
+hipError_t launch_split_rows(const float *x, int M, int K, const SplitOut &o, hipStream_t s);
 
 hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipStream_t s);
 

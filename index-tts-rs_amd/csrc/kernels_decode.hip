@@ -469,17 +469,29 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
   }
 }
 
+// Stores one fp32 value of a row in the GEMM's split form; the wave's 64 lanes hold one
+// 64-column group, whose sum lane 0 stores.
+__device__ inline void put_split(const SplitOut &o, size_t i, size_t gi, float v) {
+  uint32_t h, l;
+  split_f16(v, h, l);
+  o.hi[i] = (uint16_t)h;
+  o.lo[i] = (uint16_t)l;
+  const float s = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) o.gs[gi] = s;
+}
+
 template <int KVT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
                                                           const void *vc, int max_seq, int d,
-                                                          float *out) {
+                                                          SplitOut out) {
   __shared__ float p_lds[64];
   const int h = blockIdx.x, t = blockIdx.y;
   const size_t hb = (size_t)h * max_seq * 64;
   float m, l, o;
   attn_range<KVT>(q + (size_t)t * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), 0, base + t + 1,
                   m, l, o, p_lds);
-  out[(size_t)t * d + h * 64 + threadIdx.x] = o / l;
+  // one head is one 64-column group of the c_proj input
+  put_split(out, (size_t)t * d + h * 64 + threadIdx.x, (size_t)t * (d / 64) + h, o / l);
 }
 
 // ---------------------------------------------------------------------------------
@@ -506,12 +518,14 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const EmbedRow *rows, c
   }
 }
 
+// d is a multiple of 64, so each wave's 64 consecutive columns are one group.
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, const float *w, const float *b,
-                                                      int d, float *y) {
+                                                      int d, SplitOut y) {
   extern __shared__ float smem[];
   float *red = smem + d;
   layernorm_to_lds<256>(x + (size_t)blockIdx.x * d, w, b, d, smem, red);
-  for (int i = threadIdx.x; i < d; i += 256) y[(size_t)blockIdx.x * d + i] = smem[i];
+  for (int i = threadIdx.x; i < d; i += 256)
+    put_split(y, (size_t)blockIdx.x * d + i, (size_t)blockIdx.x * (d / 64) + i / 64, smem[i]);
 }
 
 }  // namespace
@@ -549,7 +563,7 @@ hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, in
 }
 
 hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
-                               int n_head, int max_seq, float *out, int kvt, hipStream_t s) {
+                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
   dim3 grid(n_head, T);
   const int d = n_head * 64;
   if (kvt == kKvBf16) {
@@ -570,7 +584,8 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
 }
 
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
-                          float *y, hipStream_t s) {
+                          const SplitOut &y, hipStream_t s) {
+  if (d % 64 != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, d, y);
   return hipGetLastError();
 }

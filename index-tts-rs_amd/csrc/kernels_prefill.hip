@@ -1,196 +1,443 @@
-// Prefill GEMM for gfx950 and the standalone dequantiser.
+// Prefill GEMM for gfx950, the activation splitter and the standalone dequantiser.
 //
 // The GEMM contracts M activation rows against the int8 (or int4) codes on the MFMA
-// units (v_mfma_f32_32x32x16_bf16).  Codes 0..255 are exact in bf16, so the matrix
-// cores see the true integer weights; the activations enter as a bf16 hi/lo pair
-// (x = hi + lo, ~16 significant bits) and both halves are accumulated in fp32.  The
-// MLX group affine is applied per 64-wide K group on the fp32 partial:
+// units (v_mfma_f32_32x32x16_f16).  Codes are exact in fp16, so the matrix cores see the
+// true integer weights; activations arrive pre-split as an fp16 pair x = hi + lo (~22
+// significant bits) together with their per-64-group row sums, and both halves are
+// accumulated in fp32.  The MLX group affine is applied per K group on the fp32 partial:
 //   acc += s[n,g] * (sum_{k in g} x[m,k] q[n,k]) + b[n,g] * (sum_{k in g} x[m,k]).
-// Tiles: 64(M) x 64(N) per 256-thread block, 2x2 waves of 32x32, K step = one group.
+// 4-bit codes enter as the fp16 values 16 + q (bit pattern 0x4C00 | q << 6), so the group
+// term uses b - 16 s in place of b.
+//
+// Block: 256 threads, 2 x 2 waves of (32 TM) x (32 TN) outputs, tile (64 TM) x (64 TN).
+// The K loop runs over 64-wide groups through an NS-stage ring of LDS buffers filled by
+// global->LDS DMA (no registers); each stage holds the hi/lo activation tile, the code
+// tile, the group sums and the (scale, bias) pairs.  Activation and code rows are XOR
+// swizzled in 16-byte chunks so that the MFMA fragment reads spread over the banks.
+// Small M is spread over the chip by splitting K: each split stores its partial tile,
+// and the last split to arrive at a tile (wrapping counter) adds the partials in split
+// order, so the result does not depend on arrival order.
 #include "kernels.h"
 
 namespace itts {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
 
-constexpr int BM = 64, BN = 64, BK = 64;
+template <int BITS, int PT, int TM, int TN>
+struct Shape {
+  static constexpr int BM = 64 * TM, BN = 64 * TN;
+  static constexpr int RB = BITS * 8;                          // code bytes per row per group
+  static constexpr int A_BYTES = BM * 128;                     // one fp16 plane: 64 values a row
+  static constexpr int B_BYTES = BN * RB;
+  static constexpr int P_BYTES = BN * (PT == kParamF32 ? 8 : 4);
+  static constexpr int OFF_LO = A_BYTES, OFF_B = 2 * A_BYTES, OFF_G = OFF_B + B_BYTES;
+  static constexpr int OFF_P = OFF_G + BM * 4, OFF_D = OFF_P + P_BYTES;
+  static constexpr int STAGE = OFF_D + 256;                    // + one copy target for padding jobs
+  // DMA jobs per stage: 16-byte-per-lane copies of 1 KiB (A planes, codes) and
+  // 4-byte-per-lane copies of 256 B (group sums, params), dealt round-robin to the waves
+  static constexpr int nA = BM / 4, nB = B_BYTES / 1024, nG = BM / 64, nP = P_BYTES / 256;
+  static constexpr int JOBS = nA + nB + nG + nP, PW = (JOBS + 3) / 4;
+  static_assert(B_BYTES % 1024 == 0 && P_BYTES % 256 == 0, "tile shape");
+};
 
-__device__ inline uint32_t bf16_pair_from_bytes(uint32_t w, int sh) {
-  // two consecutive codes (bits sh..sh+15 of w) -> packed bf16 pair (exact)
+__device__ __forceinline__ int swz_codes(int bits, int r) { return bits == 8 ? (r >> 2) & 3 : (r >> 3) & 1; }
+
+// two consecutive 8-bit codes (bits sh..sh+15 of w) -> packed fp16 pair (exact)
+__device__ __forceinline__ uint32_t f16_pair_u8(uint32_t w, int sh) {
   const float lo = (float)((w >> sh) & 0xffu);
   const float hi = (float)((w >> (sh + 8)) & 0xffu);
-  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
-template <int BITS, int PT, int EPI, int KVT>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As_hi[BM][BK + 8];
-  __shared__ __attribute__((aligned(16))) uint16_t As_lo[BM][BK + 8];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[BN][BK + 16];
-  __shared__ float xs[BM];
-  __shared__ float2 prm[BN];
+// the two nibbles of byte sh/8 of w -> packed fp16 pair (16 + q_even, 16 + q_odd)
+__device__ __forceinline__ uint32_t f16_pair_u4(uint32_t w, int sh) {
+  const uint32_t b = (w >> sh) & 0xffu;
+  return (((b | (b << 12)) & 0x000f000fu) << 6) | 0x4C004C00u;
+}
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+// Global->LDS copies issued by hand: lane l's bytes land at lds + l * size.  The
+// compiler cannot tell which ring buffer a pending copy targets, so the builtin makes it
+// wait for every copy in flight before any LDS read; issued here, the copies are counted
+// by the kernel's own vmcnt waits instead.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(lds_ptr)(p);
+}
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+struct Tile {
+  int tn, tm, ks;
+};
+
+template <int BITS, int PT, int EPI, int KVT, int TM, int TN, int NS>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN, int mt, int S, int gps) {
+  using Sh = Shape<BITS, PT, TM, TN>;
+  constexpr int BM = Sh::BM, BN = Sh::BN, PW = Sh::PW;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  __shared__ uint32_t last_flag;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int K = a.ql.K, N = a.ql.N, M = a.M, G = K / kGroup;
 
-  floatx16 acc;
-#pragma unroll
-  for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+  // block -> (N tile, M tile, K split).  mode 1 (few M tiles): blocks that read the same
+  // codes sit on one XCD (dispatch deals blocks to the 8 XCDs round-robin).
+  Tile t;
+  {
+    const int b = blockIdx.x;
+    if (mode == 1) {
+      const int y = b >> 3;
+      const int w = (y / mt) * 8 + (b & 7);
+      if (w >= nN * S) return;
+      t.tm = y % mt;
+      t.tn = w / S;
+      t.ks = w - t.tn * S;
+    } else {
+      t.tn = b % nN;
+      const int r = b / nN;
+      t.tm = r % mt;
+      t.ks = r / mt;
+    }
+  }
+  const int m0 = t.tm * BM, n0 = t.tn * BN;
+  const int g0 = t.ks * gps, ng = min(G, g0 + gps) - g0;
 
-  const int lr = tid >> 2, lc = (tid & 3) * 16;  // tile loader: row, first column
-  for (int g = 0; g < G; g++) {
-    {  // activations: 16 values of row lr -> bf16 hi/lo + group sum
-      const int m = m0 + lr;
-      float v[16];
-      if (m < M) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)m * K + (size_t)g * BK + lc);
+  const uint8_t *codes = a.ql.codes;
+  const size_t code_row = (size_t)K * BITS / 8;
+
+  // one stage's copies: exactly PW DMA instructions per wave, so vmcnt counts stages
+  auto issue = [&](int g, char *st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float4 f = src[i];
-          v[4 * i] = f.x;
-          v[4 * i + 1] = f.y;
-          v[4 * i + 2] = f.z;
-          v[4 * i + 3] = f.w;
+    for (int s = 0; s < PW; s++) {
+      const int j = s * 4 + wave;
+      if (j < Sh::nA) {
+        const int plane = j / (BM / 8), c1k = j % (BM / 8);
+        const int r = c1k * 8 + (lane >> 3);
+        const int lc = (lane & 7) ^ (r & 7);
+        const int m = min(m0 + r, M - 1);
+        const uint16_t *src = (plane ? a.x.lo : a.x.hi) + (size_t)m * K + g * kGroup + lc * 8;
+        dma16(src, lds_addr(st + plane * Sh::A_BYTES + c1k * 1024));
+      } else if (j < Sh::nA + Sh::nB) {
+        constexpr int CR = Sh::RB / 16, RPB = 1024 / Sh::RB;
+        const int jb = j - Sh::nA;
+        const int r = jb * RPB + lane / CR;
+        const int lc = (lane % CR) ^ swz_codes(BITS, r);
+        const int n = min(n0 + r, N - 1);
+        const uint8_t *src = codes + (size_t)n * code_row + g * Sh::RB + lc * 16;
+        dma16(src, lds_addr(st + Sh::OFF_B + jb * 1024));
+      } else if (j < Sh::nA + Sh::nB + Sh::nG) {
+        const int jg = j - Sh::nA - Sh::nB;
+        const int m = min(m0 + jg * 64 + lane, M - 1);
+        dma4(a.x.gs + (size_t)m * G + g, lds_addr(st + Sh::OFF_G + jg * 256));
+      } else if (j < Sh::JOBS) {
+        const int jp = j - Sh::nA - Sh::nB - Sh::nG;
+        const int e = jp * 64 + lane;
+        if constexpr (PT == kParamF32) {
+          const int n = min(n0 + (e >> 1), N - 1);
+          const float *src = static_cast<const float *>(a.ql.params) + ((size_t)n * G + g) * 2 + (e & 1);
+          dma4(src, lds_addr(st + Sh::OFF_P + jp * 256));
+        } else {
+          const int n = min(n0 + e, N - 1);
+          const uint32_t *src = static_cast<const uint32_t *>(a.ql.params) + (size_t)n * G + g;
+          dma4(src, lds_addr(st + Sh::OFF_P + jp * 256));
         }
       } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = 0.0f;
-      }
-      float s = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; i++) s += v[i];
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      if ((tid & 3) == 0) xs[lr] = s;
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const uint32_t hb = float_to_bf16_bits(v[i]);
-        const float lo = v[i] - __uint_as_float(hb << 16);
-        As_hi[lr][lc + i] = (uint16_t)hb;
-        As_lo[lr][lc + i] = (uint16_t)float_to_bf16_bits(lo);
+        dma4(a.x.gs + g, lds_addr(st + Sh::OFF_D));
       }
     }
-    {  // codes of row lr, 16 elements from column lc of this group
-      const int n = n0 + lr;
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if constexpr (BITS == 8) {
-        if (n < N) u = *reinterpret_cast<const uint4 *>(a.ql.codes + (size_t)n * K + (size_t)g * BK + lc);
-      } else {
-        if (n < N) {
-          const uint2 p = *reinterpret_cast<const uint2 *>(a.ql.codes + (size_t)n * (K / 2) +
-                                                            (size_t)g * (BK / 2) + lc / 2);
-          const uint32_t w2[2] = {p.x, p.y};
-          uint32_t o[4];
-#pragma unroll
-          for (int i = 0; i < 2; i++) {
-            const uint32_t w = w2[i];
-            o[2 * i] = (w & 0xfu) | ((w >> 4) & 0xfu) << 8 | ((w >> 8) & 0xfu) << 16 | ((w >> 12) & 0xfu) << 24;
-            o[2 * i + 1] = ((w >> 16) & 0xfu) | ((w >> 20) & 0xfu) << 8 | ((w >> 24) & 0xfu) << 16 |
-                           ((w >> 28) & 0xfu) << 24;
-          }
-          u = make_uint4(o[0], o[1], o[2], o[3]);
-        }
-      }
-      *reinterpret_cast<uint4 *>(&Bs[lr][lc]) = u;
-    }
-    if (tid < BN) {
-      const int n = n0 + tid;
-      prm[tid] = n < N ? load_param<PT>(a.ql.params, (size_t)n * G + g) : make_float2(0.0f, 0.0f);
-    }
-    __syncthreads();
+  };
 
-    floatx16 P;
+  floatx16 acc[TM][TN], P0[TM][TN], P1[TM][TN];
+  float2 sbp[TN];
+  floatx4 gsp[TM][4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) P[i] = 0.0f;
-    const int arow = wm * 32 + (lane & 31);
-    const int brow = wn * 32 + (lane & 31);
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; kk++) {
-      const int kof = kk * 16 + (lane >> 5) * 8;
-      const bf16x8 ahi = *reinterpret_cast<const bf16x8 *>(&As_hi[arow][kof]);
-      const bf16x8 alo = *reinterpret_cast<const bf16x8 *>(&As_lo[arow][kof]);
-      const uint2 bq = *reinterpret_cast<const uint2 *>(&Bs[brow][kof]);
-      u32x4 bw;
-      bw[0] = bf16_pair_from_bytes(bq.x, 0);
-      bw[1] = bf16_pair_from_bytes(bq.x, 16);
-      bw[2] = bf16_pair_from_bytes(bq.y, 0);
-      bw[3] = bf16_pair_from_bytes(bq.y, 16);
-      const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
-      P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi, b, P, 0, 0, 0);
-      P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo, b, P, 0, 0, 0);
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+  auto mma = [&](const char *st, floatx16(&P)[TM][TN]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) P[i][j][e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      f16x8 ah[TM], al[TM], bq[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const int row = wm * 32 * TM + i * 32 + (lane & 31);
+        const int c = kk * 2 + (lane >> 5);
+        const int off = row * 128 + ((c ^ (row & 7)) << 4);
+        ah[i] = *reinterpret_cast<const f16x8 *>(st + off);
+        al[i] = *reinterpret_cast<const f16x8 *>(st + Sh::OFF_LO + off);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int nr = wn * 32 * TN + j * 32 + (lane & 31);
+        u32x4 bw;
+        if constexpr (BITS == 8) {
+          const uint2 q = *reinterpret_cast<const uint2 *>(st + Sh::OFF_B + nr * 64 + ((kk ^ swz_codes(8, nr)) << 4) +
+                                                           (lane >> 5) * 8);
+          bw[0] = f16_pair_u8(q.x, 0);
+          bw[1] = f16_pair_u8(q.x, 16);
+          bw[2] = f16_pair_u8(q.y, 0);
+          bw[3] = f16_pair_u8(q.y, 16);
+        } else {
+          const uint32_t q = *reinterpret_cast<const uint32_t *>(
+              st + Sh::OFF_B + nr * 32 + (((kk >> 1) ^ swz_codes(4, nr)) << 4) + (kk & 1) * 8 + (lane >> 5) * 4);
+          bw[0] = f16_pair_u4(q, 0);
+          bw[1] = f16_pair_u4(q, 8);
+          bw[2] = f16_pair_u4(q, 16);
+          bw[3] = f16_pair_u4(q, 24);
+        }
+        bq[j] = __builtin_bit_cast(f16x8, bw);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bq[j], P[i][j], 0, 0, 0);
+          P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bq[j], P[i][j], 0, 0, 0);
+        }
     }
-    const float2 sb = prm[wn * 32 + (lane & 31)];
+  };
+
+  // (scale, bias) of this wave's columns and group sums of its rows, for the group in st
+  auto read_group = [&](const char *st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int r = wm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      acc[i] += sb.x * P[i] + sb.y * xs[r];
+    for (int j = 0; j < TN; j++) {
+      const int nr = wn * 32 * TN + j * 32 + (lane & 31);
+      float2 sb;
+      if constexpr (PT == kParamF32) {
+        sb = *reinterpret_cast<const float2 *>(st + Sh::OFF_P + nr * 8);
+      } else {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(st + Sh::OFF_P + nr * 4);
+        sb = make_float2(half_bits_to_float(w & 0xffffu), half_bits_to_float(w >> 16));
+      }
+      if constexpr (BITS == 4) sb.y = sb.y - 16.0f * sb.x;
+      sbp[j] = sb;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int rb = wm * 32 * TM + i * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; q++) gsp[i][q] = *reinterpret_cast<const floatx4 *>(st + Sh::OFF_G + (rb + q * 8) * 4);
+    }
+  };
+
+  auto apply = [&](const floatx16(&P)[TM][TN]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+          acc[i][j][e] = fmaf(sbp[j].x, P[i][j][e], fmaf(sbp[j].y, gsp[i][e >> 2][e & 3], acc[i][j][e]));
+  };
+
+  auto stage = [&](int i) __attribute__((always_inline)) { return lds + (i % NS) * Sh::STAGE; };
+
+  // group i: wait for its copies, start the copies NS-1 groups ahead into the buffer that
+  // group i-1 used, contract, then fold group i-1's partial (its params were read into
+  // registers while the buffer was still valid)
+  auto step = [&](int i, floatx16(&Pc)[TM][TN], const floatx16(&Pp)[TM][TN]) __attribute__((always_inline)) {
+    const int ahead = min(NS - 2, ng - 1 - i);
+    if (ahead <= 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (ahead == 1) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PW) : "memory");
     }
     __syncthreads();
+    if (i + NS - 1 < ng) issue(g0 + i + NS - 1, stage(i + NS - 1));
+    mma(stage(i), Pc);
+    if (i > 0) apply(Pp);
+    read_group(stage(i));
+  };
+
+  for (int i = 0; i < NS - 1 && i < ng; i++) issue(g0 + i, stage(i));
+  int i = 0;
+  for (; i + 1 < ng; i += 2) {
+    step(i, P0, P1);
+    step(i + 1, P1, P0);
+  }
+  if (i < ng) {
+    step(i, P0, P1);
+    apply(P0);
+  } else {
+    apply(P1);
   }
 
-  const int n = n0 + wn * 32 + (lane & 31);
-  if (n >= N) return;
-  const float bias = a.ql.bias[n];
+  const int tile = t.tm * nN + t.tn;
+  if (S > 1) {
+    // Partial tiles in the MFMA register order (8 bytes per access, contiguous across the
+    // wave).  They travel through agent-scope (sc1) stores and loads, which are coherent
+    // across the XCDs' L2s, so no L2 write-back fence is needed: each thread's stores are
+    // complete (vmcnt 0) before the block's arrival is counted, and the last block's loads
+    // are issued after it has seen the count.
+    constexpr int TILE = BM * BN;
+    uint64_t *wsb = reinterpret_cast<uint64_t *>(a.ws + (size_t)tile * S * TILE);
+    uint64_t *mine = wsb + (size_t)t.ks * (TILE / 2);
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int m = m0 + wm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-    if (m >= M) continue;
-    const float v = acc[i] + bias;
-    if constexpr (EPI == kEpiStore) {
-      a.y[(size_t)m * N + n] = v;
-    } else if constexpr (EPI == kEpiResid) {
-      a.y[(size_t)m * N + n] += v;
-    } else if constexpr (EPI == kEpiGelu) {
-      a.y[(size_t)m * N + n] = gelu_tanh(v);
-    } else {
-      const int d = a.qkv.d_model;
-      if (n < d) {
-        a.qkv.q_out[(size_t)m * d + n] = v;
-      } else {
-        const int idx = n < 2 * d ? n - d : n - 2 * d;
-        const int h = idx >> 6, e = idx & 63;
-        const size_t ci = ((size_t)h * a.qkv.max_seq + a.qkv.pos0 + m) * kHeadDim + e;
-        void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
-        if constexpr (KVT == kKvBf16) {
-          static_cast<uint16_t *>(cache)[ci] = (uint16_t)float_to_bf16_bits(v);
-        } else {
-          static_cast<float *>(cache)[ci] = v;
+    for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+          const float2 v = make_float2(acc[i2][j][2 * h], acc[i2][j][2 * h + 1]);
+          __hip_atomic_store(mine + ((((wave * TM + i2) * TN + j) * 8 + h) * 64 + lane),
+                             __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) last_flag = atomicInc(a.cnt + tile, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
+    __syncthreads();
+    if (!last_flag) return;
+    // splits added in split order (the block's own partial from registers)
+#pragma unroll
+    for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const size_t base = (size_t)(((wave * TM + i2) * TN + j) * 8) * 64 + lane;
+        floatx16 sum;
+        for (int s2 = 0; s2 < S; s2++) {
+          floatx16 v;
+          if (s2 == t.ks) {
+            v = acc[i2][j];
+          } else {
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+              const float2 w = __builtin_bit_cast(
+                  float2, __hip_atomic_load(wsb + (size_t)s2 * (TILE / 2) + base + h * 64, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT));
+              v[2 * h] = w.x;
+              v[2 * h + 1] = w.y;
+            }
+          }
+          sum = s2 == 0 ? v : sum + v;
+        }
+        acc[i2][j] = sum;
+      }
+  }
+
+  if constexpr (EPI == kEpiGelu) {
+    // GELU tile staged in LDS, then written as the next GEMM's input: hi/lo planes and
+    // the per-64-column row sums
+    constexpr int LDT = BN + 1;
+    float *T = reinterpret_cast<float *>(lds);
+    __syncthreads();
+#pragma unroll
+    for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int cl = wn * 32 * TN + j * 32 + (lane & 31);
+        const float bias = n0 + cl < N ? a.ql.bias[n0 + cl] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          T[rl * LDT + cl] = gelu_tanh(acc[i2][j][e] + bias);
         }
       }
+    __syncthreads();
+    constexpr int GPR = BN / 64, ITEMS = BM * GPR, TPI = 256 / ITEMS, VPT = 64 / TPI;
+    static_assert(ITEMS * TPI == 256 && VPT % 8 == 0, "gelu epilogue shape");
+    const int item = tid / TPI, sub = tid % TPI;
+    const int rl = item / GPR, grp = item % GPR;
+    const int c0 = grp * 64 + sub * VPT;
+    const int m = m0 + rl, n = n0 + c0;
+    float sum = 0.0f;
+    const bool live = m < M && n < N;
+#pragma unroll
+    for (int c = 0; c < VPT; c += 8) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float v0 = T[rl * LDT + c0 + c + e], v1 = T[rl * LDT + c0 + c + e + 1];
+        sum += v0;
+        sum += v1;
+        uint32_t h0, l0, h1, l1;
+        split_f16(v0, h0, l0);
+        split_f16(v1, h1, l1);
+        hw[e >> 1] = h0 | (h1 << 16);
+        lw[e >> 1] = l0 | (l1 << 16);
+      }
+      if (live) {
+        *reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      }
     }
+#pragma unroll
+    for (int o = 1; o < TPI; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    if (live && sub == 0) a.xo.gs[(size_t)m * (N / kGroup) + n / kGroup] = sum;
+    return;
+  } else {
+#pragma unroll
+    for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int n = n0 + wn * 32 * TN + j * 32 + (lane & 31);
+        if (n >= N) continue;
+        const float bias = a.ql.bias[n];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int m = m0 + wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (m >= M) continue;
+          const float v = acc[i2][j][e] + bias;
+          if constexpr (EPI == kEpiStore) {
+            a.y[(size_t)m * N + n] = v;
+          } else if constexpr (EPI == kEpiResid) {
+            a.y[(size_t)m * N + n] += v;
+          } else {
+            const int d = a.qkv.d_model;
+            if (n < d) {
+              a.qkv.q_out[(size_t)m * d + n] = v;
+            } else {
+              const int idx = n < 2 * d ? n - d : n - 2 * d;
+              const int h = idx >> 6, e2 = idx & 63;
+              const size_t ci = ((size_t)h * a.qkv.max_seq + a.qkv.pos0 + m) * kHeadDim + e2;
+              void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
+              if constexpr (KVT == kKvBf16) {
+                static_cast<uint16_t *>(cache)[ci] = (uint16_t)float_to_bf16_bits(v);
+              } else {
+                static_cast<float *>(cache)[ci] = v;
+              }
+            }
+          }
+        }
+      }
   }
 }
 
-template <int BITS, int PT>
-hipError_t gemm_dispatch(const GemmArgs &a, int epi, int kvt, hipStream_t s) {
-  dim3 grid((a.ql.N + BN - 1) / BN, (a.M + BM - 1) / BM);
-  switch (epi) {
-    case kEpiStore:
-      hipLaunchKernelGGL((gemm_kernel<BITS, PT, kEpiStore, 0>), grid, dim3(256), 0, s, a);
-      break;
-    case kEpiResid:
-      hipLaunchKernelGGL((gemm_kernel<BITS, PT, kEpiResid, 0>), grid, dim3(256), 0, s, a);
-      break;
-    case kEpiGelu:
-      hipLaunchKernelGGL((gemm_kernel<BITS, PT, kEpiGelu, 0>), grid, dim3(256), 0, s, a);
-      break;
-    case kEpiQKV:
-      if (kvt == kKvBf16) {
-        hipLaunchKernelGGL((gemm_kernel<BITS, PT, kEpiQKV, kKvBf16>), grid, dim3(256), 0, s, a);
-      } else {
-        hipLaunchKernelGGL((gemm_kernel<BITS, PT, kEpiQKV, kKvF32>), grid, dim3(256), 0, s, a);
-      }
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+// fp32 rows [M][K] -> hi/lo fp16 planes and per-group row sums; one wave per 64-group
+__global__ __launch_bounds__(256) void split_rows_kernel(const float *x, int M, int K, SplitOut o) {
+  const int G = K / kGroup;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (item >= M * G) return;
+  const int m = item / G, g = item % G;
+  const size_t i = (size_t)m * K + g * kGroup + lane;
+  const float v = x[i];
+  uint32_t h, l;
+  split_f16(v, h, l);
+  o.hi[i] = (uint16_t)h;
+  o.lo[i] = (uint16_t)l;
+  const float s = wave_sum(v);
+  if (lane == 0) o.gs[(size_t)m * G + g] = s;
 }
 
 // out[o][k] = float(q) * s then + b: two roundings, no contraction.
@@ -213,19 +460,119 @@ __global__ __launch_bounds__(256) void dequant_kernel(DevQL ql, float *out) {
   }
 }
 
+// Tile configurations: small (64 x 64, two blocks per CU) for the prefill of one
+// utterance, large (128 x 128, one block per CU) for many rows.
+constexpr int kStages = 3;
+
+struct Plan {
+  int TM, TN, mode, nN, mt, S, gps, blocks;
+  size_t lds;
+};
+
+template <int BITS, int PT, int TM, int TN>
+constexpr size_t lds_bytes() {
+  return (size_t)kStages * Shape<BITS, PT, TM, TN>::STAGE;
+}
+
+Plan make_plan(const GemmArgs &a, int bits, int ptype) {
+  Plan p{};
+  const bool large = a.M > 512;
+  p.TM = p.TN = large ? 2 : 1;
+  const int BM = 64 * p.TM, BN = 64 * p.TN;
+  const int G = a.ql.K / kGroup;
+  p.nN = (a.ql.N + BN - 1) / BN;
+  p.mt = (a.M + BM - 1) / BM;
+  const int tiles = p.nN * p.mt;
+  const int slots = std::max(1, a.n_cu) * (large ? 1 : 2);
+  // fewest rounds x groups per split, with a fixed cost for the fill and a split
+  // reduction; partial tiles must fit the workspace
+  int bestS = 1, best = 1 << 30;
+  for (int S = 1; S <= std::min(G, 32); S++) {
+    const int gps = (G + S - 1) / S, Se = (G + gps - 1) / gps;
+    if (Se != S) continue;
+    if (S > 1 && ((size_t)tiles * S * BM * BN > a.ws_floats || tiles > a.cnt_words)) break;
+    const int rounds = (tiles * S + slots - 1) / slots;
+    const int cost = rounds * (gps + 3) + (S > 1 ? 2 : 0);
+    if (cost < best) {
+      best = cost;
+      bestS = S;
+    }
+  }
+  p.S = bestS;
+  p.gps = (G + p.S - 1) / p.S;
+  p.mode = p.mt <= 4 ? 1 : 0;
+  p.blocks = p.mode == 1 ? ((p.nN * p.S + 7) / 8) * 8 * p.mt : tiles * p.S;
+  (void)bits;
+  (void)ptype;
+  return p;
+}
+
+template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
+hipError_t launch_cfg(const GemmArgs &a, const Plan &p, hipStream_t s) {
+  auto *fn = gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages>;
+  constexpr size_t lds = lds_bytes<BITS, PT, TM, TN>();
+  static bool attr_set = false;  // per instantiation
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(256), lds, s, a, p.mode, p.nN, p.mt, p.S, p.gps);
+  return hipGetLastError();
+}
+
+template <int BITS, int PT, int EPI, int KVT>
+hipError_t launch_epi(const GemmArgs &a, const Plan &p, hipStream_t s) {
+  if (p.TM == 2) return launch_cfg<BITS, PT, EPI, KVT, 2, 2>(a, p, s);
+  return launch_cfg<BITS, PT, EPI, KVT, 1, 1>(a, p, s);
+}
+
+template <int BITS, int PT>
+hipError_t gemm_dispatch(const GemmArgs &a, const Plan &p, int epi, int kvt, hipStream_t s) {
+  switch (epi) {
+    case kEpiStore:
+      return launch_epi<BITS, PT, kEpiStore, 0>(a, p, s);
+    case kEpiResid:
+      return launch_epi<BITS, PT, kEpiResid, 0>(a, p, s);
+    case kEpiGelu:
+      return launch_epi<BITS, PT, kEpiGelu, 0>(a, p, s);
+    case kEpiQKV:
+      return kvt == kKvBf16 ? launch_epi<BITS, PT, kEpiQKV, kKvBf16>(a, p, s)
+                            : launch_epi<BITS, PT, kEpiQKV, kKvF32>(a, p, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
+size_t gemm_ws_floats(int n_cu) {
+  // split-K is only chosen while tiles x splits stay within about two rounds of blocks
+  return (size_t)4 * std::max(1, n_cu) * 64 * 64 * 4;
+}
+
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s) {
-  if (a.ql.K % kGroup != 0 || a.M <= 0) return hipErrorInvalidValue;
+  if (a.ql.K % kGroup != 0 || a.M <= 0 || a.ql.N <= 0) return hipErrorInvalidValue;
+  if (epi == kEpiGelu && a.ql.N % kGroup != 0) return hipErrorInvalidValue;
+  const Plan p = make_plan(a, bits, ptype);
+  if (p.S > 1 && (a.ws == nullptr || a.cnt == nullptr)) return hipErrorInvalidValue;
   if (bits == 8) {
-    return ptype == kParamF16 ? gemm_dispatch<8, kParamF16>(a, epi, kvt, s)
-                              : gemm_dispatch<8, kParamF32>(a, epi, kvt, s);
+    return ptype == kParamF16 ? gemm_dispatch<8, kParamF16>(a, p, epi, kvt, s)
+                              : gemm_dispatch<8, kParamF32>(a, p, epi, kvt, s);
   }
   if (bits == 4) {
-    return ptype == kParamF16 ? gemm_dispatch<4, kParamF16>(a, epi, kvt, s)
-                              : gemm_dispatch<4, kParamF32>(a, epi, kvt, s);
+    return ptype == kParamF16 ? gemm_dispatch<4, kParamF16>(a, p, epi, kvt, s)
+                              : gemm_dispatch<4, kParamF32>(a, p, epi, kvt, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_split_rows(const float *x, int M, int K, const SplitOut &o, hipStream_t s) {
+  if (K % kGroup != 0 || M <= 0) return hipErrorInvalidValue;
+  const int items = M * (K / kGroup);
+  hipLaunchKernelGGL(split_rows_kernel, dim3((items + 3) / 4), dim3(256), 0, s, x, M, K, o);
+  return hipGetLastError();
 }
 
 hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipStream_t s) {

@@ -78,6 +78,19 @@ struct DevBuf {
   }
 };
 
+// Activation rows in the prefill GEMM's split form (bf16 hi/lo planes + group sums).
+struct SplitBuf {
+  DevBuf hi, lo, gs;
+  hipError_t ensure(size_t M, int K) {
+    hipError_t e = hi.ensure(sizeof(uint16_t) * M * K);
+    if (e == hipSuccess) e = lo.ensure(sizeof(uint16_t) * M * K);
+    if (e == hipSuccess) e = gs.ensure(sizeof(float) * M * (K / 64));
+    return e;
+  }
+  SplitOut out() const { return SplitOut{hi.as<uint16_t>(), lo.as<uint16_t>(), gs.as<float>()}; }
+  SplitAct act() const { return out().act(); }
+};
+
 bool valid_config(const itts_config &c, std::string &why) {
   char b[256];
   auto fail = [&](const char *m) {
@@ -135,8 +148,11 @@ struct itts_gpt {
   itts_decode_path path = ITTS_DECODE_AUTO;
   // decode workspace
   DevBuf x, q, a, f, logits;
-  // prefill workspace (grown on demand)
-  DevBuf px, ph, pq, pa, pf, rows, conds;
+  // prefill workspace (grown on demand): residual stream and q (fp32), GEMM inputs in
+  // split form (LN output, attention output, GELU output), split-K partials and counters
+  DevBuf px, pq, rows, conds;
+  SplitBuf ph, pa, pf;
+  DevBuf gws, gcnt;
   // sampler API scratch
   DevBuf s_logits, s_seen, s_rng, s_tok;
   int ptype() const { return cfg.param_dtype == ITTS_F32 ? kParamF32 : kParamF16; }
@@ -242,42 +258,40 @@ DevSampling to_dev_sampling(const itts_sampling &p, int n) {
 // cache positions 0..T-1) and the head of the last row into gpt->logits.
 itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
   const itts_config &c = g->cfg;
-  const int d = c.d_model, F = c.d_ffn, bits = c.quant_bits, pt = g->ptype();
+  const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
-  float *X = g->px.as<float>(), *Hn = g->ph.as<float>(), *Q = g->pq.as<float>();
-  float *A = g->pa.as<float>(), *Fb = g->pf.as<float>();
+  float *X = g->px.as<float>(), *Q = g->pq.as<float>();
+  auto gemm = [&](const DevQL &ql, SplitAct x) {
+    GemmArgs ga{};
+    ga.ql = ql;
+    ga.x = x;
+    ga.M = T;
+    ga.ws = g->gws.as<float>();
+    ga.ws_floats = g->gws.bytes / sizeof(float);
+    ga.cnt = g->gcnt.as<uint32_t>();
+    ga.cnt_words = kGemmCounters;
+    ga.n_cu = g->n_cu;
+    return ga;
+  };
   for (int l = 0; l < c.n_layer; l++) {
     const DevLayer &L = g->layers[l];
-    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, Hn, s));
-    GemmArgs ga{};
-    ga.ql = L.attn;
-    ga.x = Hn;
-    ga.M = T;
+    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, g->ph.out(), s));
+    GemmArgs ga = gemm(L.attn, g->ph.act());
     ga.qkv = QkvDst{Q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kv->kvt, s));
-    HIP_TRY(launch_attn_prefill(Q, T, 0, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, A,
+    HIP_TRY(launch_attn_prefill(Q, T, 0, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, g->pa.out(),
                                 kv->kvt, s));
-    ga = GemmArgs{};
-    ga.ql = L.proj;
-    ga.x = A;
-    ga.M = T;
+    ga = gemm(L.proj, g->pa.act());
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
-    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, T, d, Hn, s));
-    ga = GemmArgs{};
-    ga.ql = L.fc;
-    ga.x = Hn;
-    ga.M = T;
-    ga.y = Fb;
+    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, T, d, g->ph.out(), s));
+    ga = gemm(L.fc, g->ph.act());
+    ga.xo = g->pf.out();
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kv->kvt, s));
-    ga = GemmArgs{};
-    ga.ql = L.mproj;
-    ga.x = Fb;
-    ga.M = T;
+    ga = gemm(L.mproj, g->pf.act());
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
   }
-  (void)F;
   GemvArgs ha{};
   ha.ql = g->head;
   ha.x = X + (size_t)(T - 1) * d;
@@ -403,10 +417,10 @@ itts_status run_prefill(itts_gpt *g, itts_kv *kv, const int32_t *text, int32_t n
   rows.push_back({2, c.mel_vocab - 2, 0});
   for (int i = 0; i < n_prior; i++) rows.push_back({2, prior[i], i + 2});
   HIP_TRY(g->px.ensure(sizeof(float) * (size_t)T * d));
-  HIP_TRY(g->ph.ensure(sizeof(float) * (size_t)T * d));
+  HIP_TRY(g->ph.ensure(T, d));
   HIP_TRY(g->pq.ensure(sizeof(float) * (size_t)T * d));
-  HIP_TRY(g->pa.ensure(sizeof(float) * (size_t)T * d));
-  HIP_TRY(g->pf.ensure(sizeof(float) * (size_t)T * c.d_ffn));
+  HIP_TRY(g->pa.ensure(T, d));
+  HIP_TRY(g->pf.ensure(T, c.d_ffn));
   HIP_TRY(g->rows.ensure(sizeof(EmbedRow) * (size_t)T));
   HIP_TRY(g->conds.ensure(sizeof(float) * (size_t)std::max(1, n_cond) * d));
   HIP_TRY(hipMemcpyAsync(g->rows.p, rows.data(), sizeof(EmbedRow) * T, hipMemcpyHostToDevice, g->stream));
@@ -660,6 +674,9 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
     g->persist_ok = bits == 8 && coop != 0 && persist_init() == hipSuccess;
   }
+  if (g->gws.ensure(sizeof(float) * gemm_ws_floats(g->n_cu)) || g->gcnt.ensure(sizeof(uint32_t) * kGemmCounters) ||
+      hipMemset(g->gcnt.p, 0, sizeof(uint32_t) * kGemmCounters))
+    return fail(set_error(ITTS_E_DEVICE, "GEMM workspace allocation failed"));
   if (g->x.ensure(sizeof(float) * d) || g->q.ensure(sizeof(float) * d) || g->a.ensure(sizeof(float) * d) ||
       g->f.ensure(sizeof(float) * F) || g->logits.ensure(sizeof(float) * c.mel_vocab))
     return fail(set_error(ITTS_E_DEVICE, "workspace allocation failed"));
@@ -1222,12 +1239,21 @@ itts_status itts_qlinear_forward(itts_gpt *gpt, const itts_qlinear *ql, int32_t 
     a.y = dy.as<float>();
     HIP_TRY(launch_gemv(a, bits, pt, kProNone, kEpiStore, kKvBf16, gpt->stream));
   } else {
+    SplitBuf xs;
+    HIP_TRY(xs.ensure(M, K));
+    HIP_TRY(launch_split_rows(dx.as<float>(), M, K, xs.out(), gpt->stream));
     GemmArgs a{};
     a.ql = q.dev();
-    a.x = dx.as<float>();
+    a.x = xs.act();
     a.M = M;
     a.y = dy.as<float>();
+    a.ws = gpt->gws.as<float>();
+    a.ws_floats = gpt->gws.bytes / sizeof(float);
+    a.cnt = gpt->gcnt.as<uint32_t>();
+    a.cnt_words = kGemmCounters;
+    a.n_cu = gpt->n_cu;
     HIP_TRY(launch_gemm(a, bits, pt, kEpiStore, kKvBf16, gpt->stream));
+    HIP_TRY(hipStreamSynchronize(gpt->stream));
   }
   HIP_TRY(hipMemcpyAsync(y, dy.p, sizeof(float) * (size_t)M * N, hipMemcpyDeviceToHost, gpt->stream));
   HIP_TRY(hipStreamSynchronize(gpt->stream));

@@ -1,0 +1,144 @@
+"""Parity at the decoder's real shape, through the C ABI: 24 layers, d_model 1280, 20
+heads x 64, FFN 5120, 8194 Mel ids, int8 MLX-affine group-64 weights with fp16 params,
+seeded spec init (N(0, 0.02) linears, N(0, 0.02) tables).  The HIP path (prefill GEMMs,
+persistent or multi-kernel decode step, device sampler) is checked against the oracle on
+the same inputs: logits within the workload's 2e-2 max-abs bar, and greedy ids (repetition
+penalty 10, STOP masked) identical over the decode as the reference's greedy-codes test
+asks (sampler.rs:487-536) - exactly with fp32 caches, and wherever the decision margin
+exceeds the numeric noise with bf16 caches."""
+import sys
+
+import numpy as np
+import pytest
+
+import ito
+import itts_hip as H
+from itts_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def full():
+    say("[gpu] full-size decoder: weights")
+    W = synth.make_weights(synth.FULL_CONFIG, seed=11)
+    g = H.Gpt(W)
+    ito.lib.ito_set_threads(16)
+    yield W, g, ito.Model(W)
+    g.close()
+
+
+@pytest.mark.parametrize("n_cond,n_text", [(32, 64), (32, 200)])
+def test_full_prefill_logits(full, n_cond, n_text):
+    W, g, M = full
+    say(f"[gpu] full prefill {n_cond}+{n_text}")
+    pr = synth.make_prompt(W.cfg, n_cond, n_text, seed=n_text)
+    kv = g.kv_cache(2048)
+    a = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
+    b = M.prefill_after(M.kv(2048), pr.text_tokens, pr.conds, pr.lang_id)
+    err = float(np.abs(a - b).max())
+    say(f"[gpu]   max |logit diff| = {err:.3g} (logit range {float(np.abs(b).max()):.3g})")
+    assert err < LOGIT_TOL
+    kv32 = g.kv_cache(2048, H.ITTS_F32)
+    a32 = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv32)
+    b32 = M.prefill_after(M.kv(2048, kv_bf16=False), pr.text_tokens, pr.conds, pr.lang_id)
+    err32 = float(np.abs(a32 - b32).max())
+    say(f"[gpu]   fp32 KV: max |logit diff| = {err32:.3g}")
+    assert err32 < 1e-4     # what fp32 caches on both sides achieve; guards regressions
+    assert int(np.argmax(a)) == int(np.argmax(b))
+
+
+def _penalised(logits, seen, p=10.0):
+    x = logits.copy()
+    for t in seen:
+        x[t] = x[t] * p if x[t] < 0 else x[t] / p
+    x[8193] = -np.inf                      # STOP masked (min_codes)
+    return x
+
+
+def test_full_greedy_codes_identical_f32_kv(full):
+    """With the reference's fp32 KV cache, greedy ids over 48 steps are identical."""
+    W, g, M = full
+    say("[gpu] full greedy decode, fp32 KV")
+    pr = synth.make_prompt(W.cfg, 32, 64, seed=5)
+    n = 48
+    p = H.SamplingParams(greedy=True, repetition_penalty=10.0, max_mel_tokens=n)
+    kv = g.kv_cache(2048, H.ITTS_F32)
+    codes = H.generate_codes_after(g, H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, n), kv,
+                                   p, H.SamplerRng(0))
+    ref, _, _ = M.generate_codes_after(M.kv(2048, kv_bf16=False), pr.text_tokens, pr.conds, pr.lang_id, p,
+                                       0, min_codes=n)
+    assert len(codes) == n
+    assert codes.tolist() == ref.tolist()
+
+
+@pytest.mark.parametrize("path", [H.ITTS_DECODE_AUTO, H.ITTS_DECODE_MULTI])
+def test_full_greedy_bf16_kv(full, path):
+    """bf16 KV (the workload's cache): both sides round K/V to bf16, so an element whose
+    fp32 value differs in the last bits can round to the neighbouring bf16 value; logits
+    then differ by more than the fp32 paths do.  Teacher-forced on the oracle's ids, every
+    step's logits stay within the bar, and the greedy pick (penalty 10) agrees at every
+    step whose oracle top-2 margin exceeds 4x the largest logit difference seen; the
+    free-running decode is identical up to the first step inside that margin."""
+    W, g, M = full
+    say(f"[gpu] full greedy decode, bf16 KV, path {path}")
+    g.set_decode_path(path)
+    try:
+        pr = synth.make_prompt(W.cfg, 32, 64, seed=5)
+        n = 48
+        p = H.SamplingParams(greedy=True, repetition_penalty=10.0, max_mel_tokens=n)
+        ref, _, _ = M.generate_codes_after(M.kv(2048), pr.text_tokens, pr.conds, pr.lang_id, p, 0, min_codes=n)
+        ref = ref.tolist()
+        kv, okv = g.kv_cache(2048), M.kv(2048)
+        a = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
+        b = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)
+        seen, steps = {1, 8192}, []
+        for s in range(n):
+            pa, pb = _penalised(a, seen), _penalised(b, seen)
+            top = np.sort(pb)[-2:]
+            steps.append((float(np.abs(a - b).max()), float(top[1] - top[0]), int(np.argmax(pa)), int(np.argmax(pb))))
+            seen.add(ref[s])
+            if s + 1 < n:
+                a, b = g.step(kv, ref[s], s + 2), M.step(okv, ref[s], s + 2)
+        err = max(e for e, _, _, _ in steps)
+        margin = 4 * err
+        ties = [i for i, (_, gap, _, _) in enumerate(steps) if gap <= margin]
+        say(f"[gpu]   max |logit diff| {err:.3g}; steps inside the margin: {ties}")
+        assert err < LOGIT_TOL
+        for i, (_, gap, ia, ib) in enumerate(steps):
+            assert ib == ref[i]
+            if gap > margin:
+                assert ia == ib, (i, gap, margin)
+        kv = g.kv_cache(2048)
+        codes = H.generate_codes_after(g, H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, n), kv,
+                                       p, H.SamplerRng(0)).tolist()
+        upto = ties[0] if ties else n
+        assert codes[:upto] == ref[:upto]
+    finally:
+        g.set_decode_path(H.ITTS_DECODE_AUTO)
+
+
+def test_full_step_logits(full):
+    """Teacher-forced steps after a prefill: every step's logits within the bar."""
+    W, g, M = full
+    say("[gpu] full prefill + 16 steps")
+    pr = synth.make_prompt(W.cfg, 32, 64, seed=9)
+    kv = g.kv_cache(2048)
+    okv = M.kv(2048)
+    g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
+    M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)
+    rng = np.random.default_rng(3)
+    worst = 0.0
+    for i, t in enumerate(rng.integers(0, 8192, 16)):
+        a = g.step(kv, int(t), i + 2)
+        b = M.step(okv, int(t), i + 2)
+        worst = max(worst, float(np.abs(a - b).max()))
+    say(f"[gpu]   worst max |logit diff| over 16 steps = {worst:.3g}")
+    assert worst < LOGIT_TOL

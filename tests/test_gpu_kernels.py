@@ -64,16 +64,22 @@ def test_gemv_vs_fp64(gpt, bits, pd, N, K):
     _check_linear(got, q, bits, pd, x, 2e-6)
 
 
-@pytest.mark.parametrize("bits,pd", [(8, H.ITTS_F16), (4, H.ITTS_F16), (8, H.ITTS_F32)])
-@pytest.mark.parametrize("M,N,K", [(2, 37, 192), (99, 3840, 1280), (130, 1280, 5120), (64, 8194, 1280)])
+# Shapes cover: the 64 x 64 tile with and without split-K (small M), ragged N and M, the
+# 128 x 128 tile (M > 512) with and without split-K, and the head's N = 8194.
+@pytest.mark.parametrize("bits,pd", [(8, H.ITTS_F16), (4, H.ITTS_F16), (8, H.ITTS_F32), (4, H.ITTS_F32)])
+@pytest.mark.parametrize("M,N,K", [(2, 37, 192), (99, 3840, 1280), (130, 1280, 5120), (64, 8194, 1280),
+                                   (235, 1280, 1280), (600, 1280, 1280), (700, 384, 5120)])
 def test_mfma_gemm_vs_fp64(gpt, bits, pd, M, N, K):
     say(f"[gpu] gemm bits={bits} pd={pd} M={M} N={N} K={K}")
     rng = np.random.default_rng(M + N + K)
     q = _ql(rng, N, K, bits, pd)
     x = rng.standard_normal((M, K)).astype(np.float32)
     got = gpt.qlinear_forward(q.codes, q.scales, q.biases, q.bias, x, N, K, bits, pd)
-    # activations enter the MFMA as a bf16 hi/lo pair: ~2^-16 relative per element
-    _check_linear(got, q, bits, pd, x, 3e-5)
+    # activations enter the MFMA as an fp16 hi/lo pair: ~2^-22 relative per element
+    _check_linear(got, q, bits, pd, x, 4e-6)
+    # split-K partials are added in split order: repeated calls are bit-identical
+    again = gpt.qlinear_forward(q.codes, q.scales, q.biases, q.bias, x, N, K, bits, pd)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
 def _logits_case(rng, n, kind):
