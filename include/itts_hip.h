@@ -188,6 +188,38 @@ itts_status itts_gpt_prefill_after(itts_gpt *gpt, itts_kv *kv, const int32_t *te
 itts_status itts_gpt_step(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int32_t pos_idx,
                           float *logits_out);
 
+/* ---- teacher-forced replay (gpt.rs:391-422, 756-915; align/mod.rs:37-40) ---- */
+/* Gpt::teacher_forced / Gpt::code_log_probs: replays codes[0..n_codes) after the prompt
+ * with teacher forcing and writes log p(codes[i] | conds, text, codes[..i]) to
+ * log_probs_out [n_codes].  With attention_out set (teacher_forced), it also receives the
+ * text attention [n_codes][n_text + 2] averaged over the alignment heads (row i is the
+ * query that predicted codes[i]; columns <BOS>, text..., <EOS>); NULL gives
+ * code_log_probs.  The cache is scratch and left empty, as in the reference. */
+itts_status itts_gpt_teacher_forced(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens,
+                                    int32_t n_text, const float *conds, int32_t n_cond,
+                                    int32_t lang_id, const int32_t *codes, int32_t n_codes,
+                                    float *log_probs_out, float *attention_out);
+/* Gpt::alignment_attention: replays codes after prior_codes through the first alignment
+ * layers only and writes the text attention [n_codes][n_text + 2] averaged over the
+ * alignment heads.  The cache is scratch and left empty. */
+itts_status itts_gpt_alignment_attention(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens,
+                                         int32_t n_text, const float *conds, int32_t n_cond,
+                                         int32_t lang_id, const int32_t *prior_codes,
+                                         int32_t n_prior, const int32_t *codes, int32_t n_codes,
+                                         float *attention_out);
+/* The (layer, head) pairs averaged by the two calls above: n_pairs (1 or 2) pairs as
+ * layer0, head0, layer1, head1.  Default (4, 10), (5, 10) as align/mod.rs:37; the replay
+ * of alignment_attention runs layers 0..max layer. */
+itts_status itts_gpt_set_alignment_heads(itts_gpt *gpt, const int32_t *layer_head_pairs, int32_t n_pairs);
+/* One causal forward of a batch of prompts (each: conds, text, lang, prior codes as in
+ * prefill_after) producing the logits of every row of every prompt: logits_out
+ * [sum_b T_b][mel_vocab], prompts in order, T_b = n_cond + n_text + 3 + n_prior.  Rows of
+ * different prompts do not attend to each other; no cache is read or written.  This is
+ * the multi-row contraction that replay scores with, batched (no reference counterpart
+ * beyond teacher_forced's all-row logits, gpt.rs:838-846). */
+itts_status itts_gpt_forward_logits(itts_gpt *gpt, const itts_code_prompt *prompts, int32_t batch,
+                                    float *logits_out);
+
 /* ---- sampler (sampler.rs:19-284) ---- */
 uint64_t itts_rng_new(uint64_t seed);                  /* SamplerRng::new -> state */
 uint64_t itts_rng_next_u64(uint64_t *state);           /* SamplerRng::next_u64 */

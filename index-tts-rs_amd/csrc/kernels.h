@@ -87,9 +87,23 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
                              const float *text_pos, const float *mel_emb,
                              const float *mel_pos, int d, float *x, hipStream_t s);
 
-// LN of T rows [T][d] -> [T][d] in the GEMM's split form.
+// LN of T rows [T][d] -> [T][d] in the GEMM's split form; with w2/b2 a second LN follows.
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
-                          const SplitOut &y, hipStream_t s);
+                          const SplitOut &y, hipStream_t s, const float *w2 = nullptr,
+                          const float *b2 = nullptr);
+
+// Attention probe: softmax probabilities of head `head` (none when < 0) for the query rows
+// q0.. over the key columns [k0, k1): out [(rows - q0)][k1 - k0].
+struct AttnProbe {
+  int head, q0, k0, k1;
+  float *out;
+};
+// Causal attention of M concatenated rows: row t attends to keys kstart[t]..t of the
+// K/V [n_head][M][64]; the output rows are written in the GEMM's split form.
+hipError_t launch_attn_rows(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
+                            const SplitOut &out, const AttnProbe &p0, const AttnProbe &p1, int kvt, hipStream_t s);
+// out[r] = log_softmax(logits[r])[codes[r]] for R rows of V logits.
+hipError_t launch_log_softmax_pick(const float *logits, int R, int V, const int *codes, float *out, hipStream_t s);
 
 // Prefill GEMM: y = x[M][K] . Wdeq^T + bias with the same epilogues as the GEMV.
 struct GemmArgs {

@@ -494,6 +494,65 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int ba
   put_split(out, (size_t)t * d + h * 64 + threadIdx.x, (size_t)t * (d / 64) + h, o / l);
 }
 
+// Attention over concatenated sequences (replay / all-row logits): row t attends to the
+// keys kstart[t]..t of the scratch K/V [n_head][ld][64]; up to two probes export the
+// softmax probabilities of one head for the queries q0.. over the key columns [k0, k1).
+template <int KVT>
+__global__ __launch_bounds__(64) void attn_rows_kernel(const float *q, const void *kc, const void *vc, int ld,
+                                                       const int *kstart, int d, SplitOut out, AttnProbe p0,
+                                                       AttnProbe p1) {
+  __shared__ float p_lds[64];
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const size_t hb = (size_t)h * ld * 64;
+  const int j0 = kstart[t];
+  const void *kh = head_base<KVT>(kc, hb);
+  const float *qt = q + (size_t)t * d + h * 64;
+  float m, l, o;
+  attn_range<KVT>(qt, kh, head_base<KVT>(vc, hb), j0, t + 1, m, l, o, p_lds);
+  put_split(out, (size_t)t * d + h * 64 + lane, (size_t)t * (d / 64) + h, o / l);
+  for (int pi = 0; pi < 2; pi++) {
+    const AttnProbe &pr = pi == 0 ? p0 : p1;
+    if (pr.head != h || t < pr.q0) continue;
+    const int w = pr.k1 - pr.k0;
+    for (int c0 = 0; c0 < w; c0 += 64) {
+      const int c = c0 + lane, j = pr.k0 + c;
+      if (c >= w) continue;
+      float p = 0.0f;
+      if (j >= j0 && j <= t) {  // the score exactly as attn_range formed it
+        float kr[64];
+        load_row64<KVT>(kh, (size_t)j, kr);
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 64; e++) dot += qt[e] * kr[e];
+        p = __expf(dot * 0.125f - m) / l;
+      }
+      pr.out[(size_t)(t - pr.q0) * w + c] = p;
+    }
+  }
+}
+
+// log p(code_r | row r) = x[code] - max - log(sum exp(x - max)) over one logits row.
+__global__ __launch_bounds__(256) void log_softmax_pick_kernel(const float *logits, int V, const int *codes,
+                                                               float *out) {
+  __shared__ float red[8];
+  const float *x = logits + (size_t)blockIdx.x * V;
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, x[i]);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < V; i += 256) s += expf(x[i] - mx);
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float tot = (red[4] + red[5]) + (red[6] + red[7]);
+    out[blockIdx.x] = (x[codes[blockIdx.x]] - mx) - logf(tot);
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // Prefill embeddings and LayerNorm rows
 // ---------------------------------------------------------------------------------
@@ -518,12 +577,14 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const EmbedRow *rows, c
   }
 }
 
-// d is a multiple of 64, so each wave's 64 consecutive columns are one group.
+// d is a multiple of 64, so each wave's 64 consecutive columns are one group.  With w2
+// set, a second LayerNorm follows (ln_f then final_norm before the head).
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, const float *w, const float *b,
-                                                      int d, SplitOut y) {
+                                                      const float *w2, const float *b2, int d, SplitOut y) {
   extern __shared__ float smem[];
   float *red = smem + d;
   layernorm_to_lds<256>(x + (size_t)blockIdx.x * d, w, b, d, smem, red);
+  if (w2) layernorm_lds_inplace<256>(smem, w2, b2, d, red);
   for (int i = threadIdx.x; i < d; i += 256)
     put_split(y, (size_t)blockIdx.x * d + i, (size_t)blockIdx.x * (d / 64) + i / 64, smem[i]);
 }
@@ -584,9 +645,26 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
 }
 
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
-                          const SplitOut &y, hipStream_t s) {
+                          const SplitOut &y, hipStream_t s, const float *w2, const float *b2) {
   if (d % 64 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, d, y);
+  hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, w2, b2, d, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_rows(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
+                            const SplitOut &out, const AttnProbe &p0, const AttnProbe &p1, int kvt, hipStream_t s) {
+  dim3 grid(n_head, M);
+  const int d = n_head * 64;
+  if (kvt == kKvBf16) {
+    hipLaunchKernelGGL(attn_rows_kernel<kKvBf16>, grid, dim3(64), 0, s, q, kc, vc, M, kstart, d, out, p0, p1);
+  } else {
+    hipLaunchKernelGGL(attn_rows_kernel<kKvF32>, grid, dim3(64), 0, s, q, kc, vc, M, kstart, d, out, p0, p1);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_log_softmax_pick(const float *logits, int R, int V, const int *codes, float *out, hipStream_t s) {
+  hipLaunchKernelGGL(log_softmax_pick_kernel, dim3(R), dim3(256), 0, s, logits, V, codes, out);
   return hipGetLastError();
 }
 

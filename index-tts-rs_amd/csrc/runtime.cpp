@@ -153,6 +153,11 @@ struct itts_gpt {
   DevBuf px, pq, rows, conds;
   SplitBuf ph, pa, pf;
   DevBuf gws, gcnt;
+  // replay / all-row forward: per-layer scratch K/V (fp32 [n_head][M][64]), key starts,
+  // head logits, probe maps, codes and log-probabilities
+  DevBuf rk, rv, kstart, plog, pmap, pcodes, plp;
+  int align_pairs[2][2] = {{4, 10}, {5, 10}};  // (layer, head), align/mod.rs:37
+  int n_align = 2;
   // sampler API scratch
   DevBuf s_logits, s_seen, s_rng, s_tok;
   int ptype() const { return cfg.param_dtype == ITTS_F32 ? kParamF32 : kParamF16; }
@@ -254,6 +259,90 @@ DevSampling to_dev_sampling(const itts_sampling &p, int n) {
   return d;
 }
 
+// GEMM arguments over M rows with the decoder's split-K workspace.
+GemmArgs gemm_args(const itts_gpt *g, const DevQL &ql, SplitAct x, int M) {
+  GemmArgs ga{};
+  ga.ql = ql;
+  ga.x = x;
+  ga.M = M;
+  ga.ws = g->gws.as<float>();
+  ga.ws_floats = g->gws.bytes / sizeof(float);
+  ga.cnt = g->gcnt.as<uint32_t>();
+  ga.cnt_words = kGemmCounters;
+  ga.n_cu = g->n_cu;
+  return ga;
+}
+
+// Grows the per-row buffers of a multi-row forward to M rows.
+itts_status ensure_rows(itts_gpt *g, int M) {
+  const int d = g->cfg.d_model;
+  HIP_TRY(g->px.ensure(sizeof(float) * (size_t)M * d));
+  HIP_TRY(g->ph.ensure(M, d));
+  HIP_TRY(g->pq.ensure(sizeof(float) * (size_t)M * d));
+  HIP_TRY(g->pa.ensure(M, d));
+  HIP_TRY(g->pf.ensure(M, g->cfg.d_ffn));
+  return ITTS_OK;
+}
+
+itts_status validate_prefix(const itts_config &c, const int32_t *text, int32_t n_text,
+                            const float *conds, int32_t n_cond, int32_t max_cond, int32_t lang,
+                            const int32_t *prior, int32_t n_prior);
+
+// Embeds prompts into consecutive row ranges of gpt->px (gpt.rs:535-627 per prompt):
+// prompt b occupies rows row0[b] .. row0[b] + T[b] - 1.  Prompts are validated first.
+itts_status embed_prompts(itts_gpt *g, const itts_code_prompt *ps, int B, std::vector<int> &row0,
+                          std::vector<int> &T, int *M_out) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model;
+  int M = 0, n_cond_all = 0;
+  row0.assign(B, 0);
+  T.assign(B, 0);
+  for (int b = 0; b < B; b++) {
+    const itts_code_prompt &p = ps[b];
+    if (itts_status st = validate_prefix(c, p.text_tokens, p.n_text, p.conds, p.n_cond, g->max_cond, p.lang_id,
+                                         p.prior_codes, p.n_prior))
+      return st;
+    row0[b] = M;
+    T[b] = p.n_cond + p.n_text + 3 + p.n_prior;
+    M += T[b];
+    n_cond_all += p.n_cond;
+  }
+  std::vector<EmbedRow> rows;
+  rows.reserve(M);
+  int cbase = 0;
+  for (int b = 0; b < B; b++) {
+    const itts_code_prompt &p = ps[b];
+    for (int i = 0; i < p.n_cond; i++) rows.push_back({0, cbase + i, 0});
+    for (int j = 0; j < p.n_text + 2; j++) {
+      const int u = j == 0 ? 0 : (j == p.n_text + 1 ? 1 : p.text_tokens[j - 1]);
+      rows.push_back({1, u, j});
+    }
+    rows.push_back({2, c.mel_vocab - 2, 0});
+    for (int i = 0; i < p.n_prior; i++) rows.push_back({2, p.prior_codes[i], i + 2});
+    cbase += p.n_cond;
+  }
+  if (itts_status st = ensure_rows(g, M)) return st;
+  HIP_TRY(g->rows.ensure(sizeof(EmbedRow) * (size_t)M));
+  HIP_TRY(g->conds.ensure(sizeof(float) * (size_t)std::max(1, n_cond_all) * d));
+  HIP_TRY(hipMemcpyAsync(g->rows.p, rows.data(), sizeof(EmbedRow) * M, hipMemcpyHostToDevice, g->stream));
+  cbase = 0;
+  for (int b = 0; b < B; b++) {
+    const itts_code_prompt &p = ps[b];
+    if (p.n_cond > 0)
+      HIP_TRY(hipMemcpyAsync(g->conds.as<float>() + (size_t)cbase * d, p.conds, sizeof(float) * (size_t)p.n_cond * d,
+                             hipMemcpyHostToDevice, g->stream));
+    HIP_TRY(launch_embed_rows(g->rows.as<EmbedRow>() + row0[b], T[b], g->conds.as<float>(), g->text_emb.as<float>(),
+                              g->lang_emb.as<float>() + (size_t)p.lang_id * d, g->text_pos.as<float>(),
+                              g->mel_emb.as<float>(), g->mel_pos.as<float>(), d,
+                              g->px.as<float>() + (size_t)row0[b] * d, g->stream));
+    cbase += p.n_cond;
+  }
+  // the host arrays above are staged by the copies before they return
+  HIP_TRY(hipStreamSynchronize(g->stream));
+  *M_out = M;
+  return ITTS_OK;
+}
+
 // Enqueues the stack over the rows already embedded in gpt->px (prefill, T rows at
 // cache positions 0..T-1) and the head of the last row into gpt->logits.
 itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
@@ -261,18 +350,7 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
   const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
   float *X = g->px.as<float>(), *Q = g->pq.as<float>();
-  auto gemm = [&](const DevQL &ql, SplitAct x) {
-    GemmArgs ga{};
-    ga.ql = ql;
-    ga.x = x;
-    ga.M = T;
-    ga.ws = g->gws.as<float>();
-    ga.ws_floats = g->gws.bytes / sizeof(float);
-    ga.cnt = g->gcnt.as<uint32_t>();
-    ga.cnt_words = kGemmCounters;
-    ga.n_cu = g->n_cu;
-    return ga;
-  };
+  auto gemm = [&](const DevQL &ql, SplitAct x) { return gemm_args(g, ql, x, T); };
   for (int l = 0; l < c.n_layer; l++) {
     const DevLayer &L = g->layers[l];
     HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, g->ph.out(), s));
@@ -401,40 +479,129 @@ itts_status run_prefill(itts_gpt *g, itts_kv *kv, const int32_t *text, int32_t n
   const itts_config &c = g->cfg;
   itts_status st = validate_prefix(c, text, n_text, conds, n_cond, g->max_cond, lang, prior, n_prior);
   if (st) return st;
-  const int d = c.d_model;
   const int T = n_cond + n_text + 3 + n_prior;
   kv->valid_len = 0;
   if (T > kv->max_seq)
     return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d", T,
                      kv->max_seq);
-  std::vector<EmbedRow> rows;
-  rows.reserve(T);
-  for (int i = 0; i < n_cond; i++) rows.push_back({0, i, 0});
-  for (int j = 0; j < n_text + 2; j++) {
-    const int u = j == 0 ? 0 : (j == n_text + 1 ? 1 : text[j - 1]);
-    rows.push_back({1, u, j});
-  }
-  rows.push_back({2, c.mel_vocab - 2, 0});
-  for (int i = 0; i < n_prior; i++) rows.push_back({2, prior[i], i + 2});
-  HIP_TRY(g->px.ensure(sizeof(float) * (size_t)T * d));
-  HIP_TRY(g->ph.ensure(T, d));
-  HIP_TRY(g->pq.ensure(sizeof(float) * (size_t)T * d));
-  HIP_TRY(g->pa.ensure(T, d));
-  HIP_TRY(g->pf.ensure(T, c.d_ffn));
-  HIP_TRY(g->rows.ensure(sizeof(EmbedRow) * (size_t)T));
-  HIP_TRY(g->conds.ensure(sizeof(float) * (size_t)std::max(1, n_cond) * d));
-  HIP_TRY(hipMemcpyAsync(g->rows.p, rows.data(), sizeof(EmbedRow) * T, hipMemcpyHostToDevice, g->stream));
-  if (n_cond > 0)
-    HIP_TRY(hipMemcpyAsync(g->conds.p, conds, sizeof(float) * (size_t)n_cond * d, hipMemcpyHostToDevice,
-                           g->stream));
-  HIP_TRY(launch_embed_rows(g->rows.as<EmbedRow>(), T, g->conds.as<float>(), g->text_emb.as<float>(),
-                            g->lang_emb.as<float>() + (size_t)lang * d, g->text_pos.as<float>(),
-                            g->mel_emb.as<float>(), g->mel_pos.as<float>(), d, g->px.as<float>(),
-                            g->stream));
+  const itts_code_prompt p{text, n_text, conds, n_cond, lang, prior, n_prior, 0};
+  std::vector<int> row0, Tb;
+  int M = 0;
+  if ((st = embed_prompts(g, &p, 1, row0, Tb, &M))) return st;
   st = enqueue_prefill_stack(g, kv, T);
   if (st) return st;
   kv->valid_len = T;
   *T_out = T;
+  return ITTS_OK;
+}
+
+// A requested attention export: probabilities of (layer, head) for the query rows q0..
+// over the key columns [k0, k1), into device memory.
+struct ProbeSpec {
+  int layer, head, q0, k0, k1;
+  float *out;
+};
+
+// Runs n_layers blocks over the M rows in gpt->px (row r attends to keys kstart[r]..r)
+// with fp32 scratch K/V for one layer at a time, filling the probes on the way.
+itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstart, int n_layers,
+                               const std::vector<ProbeSpec> &probes) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
+  hipStream_t s = g->stream;
+  HIP_TRY(g->rk.ensure(sizeof(float) * (size_t)M * d));
+  HIP_TRY(g->rv.ensure(sizeof(float) * (size_t)M * d));
+  HIP_TRY(g->kstart.ensure(sizeof(int) * (size_t)M));
+  HIP_TRY(hipMemcpyAsync(g->kstart.p, kstart.data(), sizeof(int) * M, hipMemcpyHostToDevice, s));
+  float *X = g->px.as<float>(), *Q = g->pq.as<float>();
+  for (int l = 0; l < n_layers; l++) {
+    const DevLayer &L = g->layers[l];
+    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, M, d, g->ph.out(), s));
+    GemmArgs ga = gemm_args(g, L.attn, g->ph.act(), M);
+    ga.qkv = QkvDst{Q, g->rk.p, g->rv.p, M, 0, d};
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kKvF32, s));
+    AttnProbe pr[2] = {{-1, 0, 0, 0, nullptr}, {-1, 0, 0, 0, nullptr}};
+    int np = 0;
+    for (const ProbeSpec &p : probes)
+      if (p.layer == l && np < 2) pr[np++] = AttnProbe{p.head, p.q0, p.k0, p.k1, p.out};
+    HIP_TRY(launch_attn_rows(Q, M, g->kstart.as<int>(), g->rk.p, g->rv.p, c.n_head, g->pa.out(), pr[0], pr[1],
+                             kKvF32, s));
+    ga = gemm_args(g, L.proj, g->pa.act(), M);
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
+    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, M, d, g->ph.out(), s));
+    ga = gemm_args(g, L.fc, g->ph.act(), M);
+    ga.xo = g->pf.out();
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kKvF32, s));
+    ga = gemm_args(g, L.mproj, g->pf.act(), M);
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
+  }
+  return ITTS_OK;
+}
+
+// Head logits of R rows of gpt->px from row0: ln_f, final_norm, mel_head (gpt.rs:838-846)
+// into gpt->plog [R][mel_vocab].
+itts_status head_rows(itts_gpt *g, int row0, int R) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model;
+  HIP_TRY(g->plog.ensure(sizeof(float) * (size_t)R * c.mel_vocab));
+  HIP_TRY(launch_ln_rows(g->px.as<float>() + (size_t)row0 * d, g->ln_f_w.as<float>(), g->ln_f_b.as<float>(), R, d,
+                         g->ph.out(), g->stream, g->fn_w.as<float>(), g->fn_b.as<float>()));
+  GemmArgs ga = gemm_args(g, g->head, g->ph.act(), R);
+  ga.y = g->plog.as<float>();
+  HIP_TRY(launch_gemm(ga, c.quant_bits, g->ptype(), kEpiStore, kKvF32, g->stream));
+  return ITTS_OK;
+}
+
+// Shared part of teacher_forced / code_log_probs / alignment_attention (gpt.rs:797-915):
+// embeds the prompt with `fed` as prior codes, runs n_layers blocks with the alignment
+// probes of queries q0.. over the text columns, and averages the maps into attention_out.
+itts_status replay(itts_gpt *g, itts_kv *kv, const int32_t *text, int32_t n_text, const float *conds,
+                   int32_t n_cond, int32_t lang, const std::vector<int32_t> &fed, int32_t q0, int n_layers,
+                   int n_codes, float *attention_out, int *T_out) {
+  const itts_config &c = g->cfg;
+  const int T = n_cond + n_text + 3 + (int)fed.size();
+  kv->valid_len = 0;  // the cache is scratch (gpt.rs:819, 836)
+  const itts_code_prompt p{text, n_text, conds, n_cond, lang, fed.empty() ? nullptr : fed.data(), (int32_t)fed.size(),
+                           0};
+  if (itts_status st = validate_prefix(c, text, n_text, conds, n_cond, g->max_cond, lang, p.prior_codes, p.n_prior))
+    return st;
+  if (T > kv->max_seq)
+    return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d", T, kv->max_seq);
+  std::vector<int> row0, Tb;
+  int M = 0;
+  if (itts_status st = embed_prompts(g, &p, 1, row0, Tb, &M)) return st;
+  const int text_lo = n_cond, text_hi = n_cond + n_text + 2, W = n_text + 2;
+  std::vector<ProbeSpec> probes;
+  if (attention_out) {
+    HIP_TRY(g->pmap.ensure(sizeof(float) * (size_t)g->n_align * n_codes * W));
+    for (int i = 0; i < g->n_align; i++)
+      probes.push_back({g->align_pairs[i][0], g->align_pairs[i][1], q0, text_lo, text_hi,
+                        g->pmap.as<float>() + (size_t)i * n_codes * W});
+  }
+  if (itts_status st = forward_rows_stack(g, M, std::vector<int>(M, 0), n_layers, probes)) return st;
+  if (attention_out) {
+    std::vector<float> maps((size_t)g->n_align * n_codes * W);
+    HIP_TRY(hipMemcpyAsync(maps.data(), g->pmap.p, sizeof(float) * maps.size(), hipMemcpyDeviceToHost, g->stream));
+    HIP_TRY(hipStreamSynchronize(g->stream));
+    const size_t n = (size_t)n_codes * W;
+    for (size_t i = 0; i < n; i++) {  // mean over the stacked maps (gpt.rs:849-851)
+      float acc = maps[i];
+      for (int k = 1; k < g->n_align; k++) acc += maps[k * n + i];
+      attention_out[i] = acc / (float)g->n_align;
+    }
+  }
+  *T_out = T;
+  return ITTS_OK;
+}
+
+itts_status check_replay_args(itts_gpt *g, itts_kv *kv, const int32_t *codes, int32_t n_codes) {
+  if (!g || !kv || kv->gpt != g) return set_error(ITTS_E_VALIDATION, "kv_cache: cache belongs to another decoder");
+  if (n_codes <= 0 || !codes) return set_error(ITTS_E_VALIDATION, "codes: codes must not be empty");
+  for (int i = 0; i < n_codes; i++)
+    if (codes[i] < 0 || codes[i] >= g->cfg.mel_vocab)
+      return set_error(ITTS_E_VALIDATION, "codes: id %d out of range 0..%d", codes[i], g->cfg.mel_vocab);
   return ITTS_OK;
 }
 
@@ -807,6 +974,96 @@ itts_status itts_gpt_prefill_after(itts_gpt *gpt, itts_kv *kv, const int32_t *te
   if (logits_out)
     HIP_TRY(hipMemcpyAsync(logits_out, gpt->logits.p, sizeof(float) * gpt->cfg.mel_vocab,
                            hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_teacher_forced(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens, int32_t n_text,
+                                    const float *conds, int32_t n_cond, int32_t lang_id, const int32_t *codes,
+                                    int32_t n_codes, float *log_probs_out, float *attention_out) {
+  if (itts_status st = check_replay_args(gpt, kv, codes, n_codes)) return st;
+  if (!log_probs_out) return set_error(ITTS_E_VALIDATION, "log_probs: null output");
+  if (attention_out)
+    for (int i = 0; i < gpt->n_align; i++)
+      if (gpt->align_pairs[i][0] >= gpt->cfg.n_layer || gpt->align_pairs[i][1] >= gpt->cfg.n_head)
+        return set_error(ITTS_E_VALIDATION, "alignment_heads: (%d, %d) outside the model", gpt->align_pairs[i][0],
+                         gpt->align_pairs[i][1]);
+  // the last code is only a target: the fed rows are codes[..n-1] (gpt.rs:806-811)
+  const std::vector<int32_t> fed(codes, codes + n_codes - 1);
+  const int text_hi = n_cond + n_text + 2;
+  int T = 0;
+  if (itts_status st = replay(gpt, kv, text_tokens, n_text, conds, n_cond, lang_id, fed, text_hi, gpt->cfg.n_layer,
+                              n_codes, attention_out, &T))
+    return st;
+  // rows text_hi .. T-1 (the start-Mel row and the fed codes) predict codes[0..n)
+  if (itts_status st = head_rows(gpt, text_hi, n_codes)) return st;
+  HIP_TRY(gpt->pcodes.ensure(sizeof(int32_t) * n_codes));
+  HIP_TRY(gpt->plp.ensure(sizeof(float) * n_codes));
+  HIP_TRY(hipMemcpyAsync(gpt->pcodes.p, codes, sizeof(int32_t) * n_codes, hipMemcpyHostToDevice, gpt->stream));
+  HIP_TRY(launch_log_softmax_pick(gpt->plog.as<float>(), n_codes, gpt->cfg.mel_vocab, gpt->pcodes.as<int>(),
+                                  gpt->plp.as<float>(), gpt->stream));
+  HIP_TRY(hipMemcpyAsync(log_probs_out, gpt->plp.p, sizeof(float) * n_codes, hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  kv->valid_len = 0;
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_alignment_attention(itts_gpt *gpt, itts_kv *kv, const int32_t *text_tokens, int32_t n_text,
+                                         const float *conds, int32_t n_cond, int32_t lang_id,
+                                         const int32_t *prior_codes, int32_t n_prior, const int32_t *codes,
+                                         int32_t n_codes, float *attention_out) {
+  if (itts_status st = check_replay_args(gpt, kv, codes, n_codes)) return st;
+  if (!attention_out) return set_error(ITTS_E_VALIDATION, "attention: null output");
+  if (n_prior < 0 || (n_prior > 0 && !prior_codes)) return set_error(ITTS_E_VALIDATION, "codes: null prior codes");
+  int n_layers = 0;
+  for (int i = 0; i < gpt->n_align; i++) {
+    if (gpt->align_pairs[i][0] >= gpt->cfg.n_layer || gpt->align_pairs[i][1] >= gpt->cfg.n_head)
+      return set_error(ITTS_E_VALIDATION, "alignment_heads: (%d, %d) outside the model", gpt->align_pairs[i][0],
+                       gpt->align_pairs[i][1]);
+    n_layers = std::max(n_layers, gpt->align_pairs[i][0] + 1);
+  }
+  // fed = prior ++ codes[..n-1]; queries from the row that predicted codes[0] (gpt.rs:885-895)
+  std::vector<int32_t> fed(prior_codes, prior_codes + n_prior);
+  fed.insert(fed.end(), codes, codes + n_codes - 1);
+  const int q0 = n_cond + n_text + 2 + n_prior;
+  int T = 0;
+  if (itts_status st = replay(gpt, kv, text_tokens, n_text, conds, n_cond, lang_id, fed, q0, n_layers, n_codes,
+                              attention_out, &T))
+    return st;
+  kv->valid_len = 0;
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_set_alignment_heads(itts_gpt *gpt, const int32_t *pairs, int32_t n_pairs) {
+  if (!gpt || !pairs || n_pairs < 1 || n_pairs > 2)
+    return set_error(ITTS_E_VALIDATION, "alignment_heads: 1 or 2 (layer, head) pairs expected");
+  for (int i = 0; i < n_pairs; i++)
+    if (pairs[2 * i] < 0 || pairs[2 * i] >= gpt->cfg.n_layer || pairs[2 * i + 1] < 0 ||
+        pairs[2 * i + 1] >= gpt->cfg.n_head)
+      return set_error(ITTS_E_VALIDATION, "alignment_heads: (%d, %d) outside the model", pairs[2 * i],
+                       pairs[2 * i + 1]);
+  for (int i = 0; i < n_pairs; i++) {
+    gpt->align_pairs[i][0] = pairs[2 * i];
+    gpt->align_pairs[i][1] = pairs[2 * i + 1];
+  }
+  gpt->n_align = n_pairs;
+  return ITTS_OK;
+}
+
+itts_status itts_gpt_forward_logits(itts_gpt *gpt, const itts_code_prompt *prompts, int32_t batch,
+                                    float *logits_out) {
+  if (!gpt || !prompts || batch <= 0 || !logits_out)
+    return set_error(ITTS_E_VALIDATION, "prompts: a non-empty batch and an output are required");
+  std::vector<int> row0, T;
+  int M = 0;
+  if (itts_status st = embed_prompts(gpt, prompts, batch, row0, T, &M)) return st;
+  std::vector<int> kstart(M);
+  for (int b = 0; b < batch; b++)
+    for (int r = 0; r < T[b]; r++) kstart[row0[b] + r] = row0[b];
+  if (itts_status st = forward_rows_stack(gpt, M, kstart, gpt->cfg.n_layer, {})) return st;
+  if (itts_status st = head_rows(gpt, 0, M)) return st;
+  HIP_TRY(hipMemcpyAsync(logits_out, gpt->plog.p, sizeof(float) * (size_t)M * gpt->cfg.mel_vocab,
+                         hipMemcpyDeviceToHost, gpt->stream));
   HIP_TRY(hipStreamSynchronize(gpt->stream));
   return ITTS_OK;
 }

@@ -132,6 +132,14 @@ _SIGS = {
     "itts_kv_decode_path": (C.c_int, [C.c_void_p]),
     "itts_gpt_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
                                    C.c_int32, C.c_int32, C.c_void_p]),
+    "itts_gpt_teacher_forced": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                          C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
+                                          C.c_void_p]),
+    "itts_gpt_alignment_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                               C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
+                                               C.c_int32, C.c_void_p]),
+    "itts_gpt_set_alignment_heads": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32]),
+    "itts_gpt_forward_logits": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
     "itts_gpt_prefill_after": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                          C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
                                          C.c_int32, C.c_void_p]),
@@ -324,6 +332,54 @@ class Gpt:
     def step(self, cache, mel_token_id, pos_idx, logits=True):
         out = np.empty(self.cfg["mel_vocab"], np.float32) if logits else None
         _check(lib.itts_gpt_step(self._h, cache._h, int(mel_token_id), int(pos_idx), _ptr(out)))
+        return out
+
+    # teacher-forced replay (gpt.rs:756-915)
+    def _tc(self, text_tokens, conds):
+        t = np.ascontiguousarray(text_tokens, dtype=np.int32)
+        c = np.ascontiguousarray(conds, dtype=np.float32).reshape(-1, self.cfg["d_model"]) \
+            if conds is not None else np.zeros((0, self.cfg["d_model"]), np.float32)
+        return t, c
+
+    def teacher_forced(self, text_tokens, conds, lang_id, codes, cache, attention=True):
+        """Gpt::teacher_forced (attention=True) / code_log_probs (False): returns
+        (log_probs [n], attention [n][n_text + 2] or None)."""
+        t, c = self._tc(text_tokens, conds)
+        cd = np.ascontiguousarray(codes, dtype=np.int32)
+        lp = np.empty(len(cd), np.float32)
+        att = np.empty((len(cd), len(t) + 2), np.float32) if attention else None
+        _check(lib.itts_gpt_teacher_forced(self._h, cache._h, _ptr(t), len(t), _ptr(c), c.shape[0], int(lang_id),
+                                           _ptr(cd), len(cd), _ptr(lp), _ptr(att)))
+        return lp, att
+
+    def code_log_probs(self, text_tokens, conds, lang_id, codes, cache):
+        return self.teacher_forced(text_tokens, conds, lang_id, codes, cache, attention=False)[0]
+
+    def alignment_attention(self, text_tokens, conds, lang_id, prior_codes, codes, cache):
+        t, c = self._tc(text_tokens, conds)
+        pr = np.ascontiguousarray(prior_codes if prior_codes is not None else [], dtype=np.int32)
+        cd = np.ascontiguousarray(codes, dtype=np.int32)
+        att = np.empty((len(cd), len(t) + 2), np.float32)
+        _check(lib.itts_gpt_alignment_attention(self._h, cache._h, _ptr(t), len(t), _ptr(c), c.shape[0],
+                                                int(lang_id), _ptr(pr), len(pr), _ptr(cd), len(cd), _ptr(att)))
+        return att
+
+    def set_alignment_heads(self, pairs):
+        a = np.ascontiguousarray(np.asarray(pairs, dtype=np.int32).reshape(-1))
+        _check(lib.itts_gpt_set_alignment_heads(self._h, _ptr(a), len(a) // 2))
+
+    def forward_logits(self, prompts):
+        """All-row logits of a batch of CodePrompts in one forward: [sum T_b][mel_vocab]."""
+        keep, arr = [], (itts_code_prompt * len(prompts))()
+        rows = 0
+        for i, p in enumerate(prompts):
+            t, c = self._tc(p.text_tokens, p.conds)
+            pr = np.ascontiguousarray(p.prior_codes if p.prior_codes is not None else [], dtype=np.int32)
+            keep += [t, c, pr]
+            arr[i] = itts_code_prompt(_ptr(t), len(t), _ptr(c), c.shape[0], int(p.lang_id), _ptr(pr), len(pr), 0)
+            rows += c.shape[0] + len(t) + 3 + len(pr)
+        out = np.empty((rows, self.cfg["mel_vocab"]), np.float32)
+        _check(lib.itts_gpt_forward_logits(self._h, C.cast(arr, C.c_void_p), len(prompts), _ptr(out)))
         return out
 
     # kernel-level helpers

@@ -51,6 +51,11 @@ class ito_model(C.Structure):
                 ("fn_w", C.c_void_p), ("fn_b", C.c_void_p), ("head", ito_ql)]
 
 
+class ito_probe(C.Structure):
+    _fields_ = [("layer", C.c_int32), ("head", C.c_int32), ("q0", C.c_int32), ("k0", C.c_int32),
+                ("k1", C.c_int32), ("out", C.c_void_p)]
+
+
 class ito_sampling(C.Structure):
     _fields_ = [("greedy", C.c_int32), ("temperature", C.c_float), ("top_p", C.c_float),
                 ("top_k", C.c_uint32), ("repetition_penalty", C.c_float),
@@ -82,6 +87,8 @@ _SIGS = {
                                     C.c_int32, C.c_int32, P, C.c_int32, P]),
     "ito_step": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, C.c_int32, C.c_int32, P]),
     "ito_forward_rows": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32, C.c_int32, P]),
+    "ito_replay": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32, C.c_int32, P, C.c_int32,
+                             C.c_int32, P]),
     "ito_sequence_embedding": (C.c_int, [C.POINTER(ito_model), P, C.c_int32, P, C.c_int32,
                                          C.c_int32, P, C.c_int32, P]),
     "ito_sampling_validate": (C.c_int, [C.POINTER(ito_sampling)]),
@@ -189,6 +196,22 @@ class Model:
         out = np.empty((T - row0, self.w.cfg["mel_vocab"]), np.float32)
         check(lib.ito_forward_rows(self.ref, kv.h, kv.mode, _p(emb), T, row0, _p(out)))
         return out
+
+    def replay(self, kv, emb, n_layers=None, probes=(), row0=None):
+        """Stack over emb [T][d] through n_layers blocks; probes are (layer, head, q0, k0, k1)
+        tuples whose attention slices [(T-q0)][k1-k0] are returned; with row0 set (whole
+        stack) also the logits of rows row0.. .  Returns (logits or None, [probe arrays])."""
+        emb = np.ascontiguousarray(emb, np.float32)
+        T = emb.shape[0]
+        n_layers = self.w.cfg["n_layer"] if n_layers is None else n_layers
+        outs = [np.zeros((T - q0, k1 - k0), np.float32) for (_, _, q0, k0, k1) in probes]
+        arr = (ito_probe * max(1, len(probes)))()
+        for i, ((l, h, q0, k0, k1), o) in enumerate(zip(probes, outs)):
+            arr[i] = ito_probe(l, h, q0, k0, k1, o.ctypes.data)
+        logits = None if row0 is None else np.empty((T - row0, self.w.cfg["mel_vocab"]), np.float32)
+        check(lib.ito_replay(self.ref, kv.h, kv.mode, _p(emb), T, n_layers, C.cast(arr, C.c_void_p),
+                             len(probes), 0 if row0 is None else row0, _p(logits)))
+        return logits, outs
 
     def generate_codes_after(self, kv, text, conds, lang_id, params, rng_state, prior=(),
                              min_codes=0):

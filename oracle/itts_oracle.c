@@ -447,6 +447,26 @@ int ito_forward_rows(const ito_model *m, ito_kv *kv, int32_t mode, const float *
                          : forward_rows__f32(m, kv, emb, T, row0, out);
 }
 
+int ito_replay(const ito_model *m, ito_kv *kv, int32_t mode, const float *emb, int32_t T,
+               int32_t n_layers, const ito_probe *probes, int32_t n_probes, int32_t row0,
+               float *logits) {
+  int rc = check_mode(kv, mode);
+  if (rc) return rc;
+  if (T <= 0 || row0 < 0 || row0 >= T || n_layers < 1 || n_layers > m->cfg.n_layer ||
+      (logits && n_layers != m->cfg.n_layer))
+    return set_err(ITO_E_VALIDATION, "bad replay range");
+  for (int i = 0; i < n_probes; i++) {
+    const ito_probe *p = &probes[i];
+    if (p->layer < 0 || p->layer >= n_layers || p->head < 0 || p->head >= m->cfg.n_head || p->q0 < 0 ||
+        p->q0 >= T || p->k0 < 0 || p->k1 <= p->k0 || p->k1 > T || !p->out)
+      return set_err(ITO_E_VALIDATION, "bad probe %d", i);
+  }
+  kv->valid_len = 0;
+  if (T > kv->max_seq) return set_err(ITO_E_CAPACITY, "kv_cache: sequence too long");
+  return mode == ITO_F64 ? replay__f64(m, kv, emb, T, n_layers, probes, n_probes, row0, logits)
+                         : replay__f32(m, kv, emb, T, n_layers, probes, n_probes, row0, logits);
+}
+
 int ito_step(const ito_model *m, ito_kv *kv, int32_t mode, int32_t tok, int32_t pos,
              float *logits) {
   int rc = check_mode(kv, mode);

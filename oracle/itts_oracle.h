@@ -124,6 +124,20 @@ int ito_step(const ito_model *m, ito_kv *kv, int32_t mode, int32_t tok, int32_t 
  * stack and return logits for rows [row0, T): out [(T-row0)][mel_vocab]. */
 int ito_forward_rows(const ito_model *m, ito_kv *kv, int32_t mode, const float *emb,
                      int32_t T, int32_t row0, float *out);
+/* Attention probe (gpt.rs:391-422 Gpt2Block::head_attention): softmax probabilities of
+ * head `head` in layer `layer` for the queries q0..T-1 over keys 0..query (causal), sliced
+ * to the key columns [k0, k1): out [(T - q0)][k1 - k0]. */
+typedef struct {
+  int32_t layer, head, q0, k0, k1;
+  float *out;
+} ito_probe;
+/* Replay (gpt.rs:797-858): the causal stack over emb [T][d] through the first n_layers
+ * blocks, filling the probes on the way; when logits != NULL (and n_layers is the whole
+ * stack) also the head's logits of rows [row0, T): [(T-row0)][mel_vocab].  The cache is
+ * scratch and left empty. */
+int ito_replay(const ito_model *m, ito_kv *kv, int32_t mode, const float *emb, int32_t T,
+               int32_t n_layers, const ito_probe *probes, int32_t n_probes, int32_t row0,
+               float *logits);
 /* Embedding rows of gpt.rs sequence_embedding: [n_cond + n_text + 3 + n_prior][d]. */
 int ito_sequence_embedding(const ito_model *m, const int32_t *text, int32_t n_text,
                            const float *conds, int32_t n_cond, int32_t lang_id,

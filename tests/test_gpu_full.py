@@ -142,3 +142,44 @@ def test_full_step_logits(full):
         worst = max(worst, float(np.abs(a - b).max()))
     say(f"[gpu]   worst max |logit diff| over 16 steps = {worst:.3g}")
     assert worst < LOGIT_TOL
+
+
+def test_full_teacher_forced(full):
+    """teacher_forced at the real shape with the reference's alignment heads (4, 10), (5, 10):
+    log-probabilities of 48 codes and the averaged text attention against the oracle."""
+    W, g, M = full
+    say("[gpu] full teacher_forced, 48 codes")
+    pr = synth.make_prompt(W.cfg, 32, 64, seed=12)
+    codes = np.random.default_rng(12).integers(0, 8192, 48).astype(np.int32)
+    lp, att = g.teacher_forced(pr.text_tokens, pr.conds, pr.lang_id, codes, g.kv_cache(2048))
+    text_lo, text_hi = 32, 32 + 64 + 2
+    emb = M.sequence_embedding(pr.text_tokens, pr.conds, pr.lang_id, codes[:-1])
+    lg, maps = M.replay(M.kv(2048, kv_bf16=False), emb,
+                        probes=[(4, 10, text_hi, text_lo, text_hi), (5, 10, text_hi, text_lo, text_hi)], row0=text_hi)
+    x = lg.astype(np.float64)
+    x -= x.max(1, keepdims=True)
+    ref = (x - np.log(np.exp(x).sum(1, keepdims=True)))[np.arange(48), codes]
+    err_lp = float(np.abs(lp - ref).max())
+    err_att = float(np.abs(att - (maps[0] + maps[1]) / 2).max())
+    say(f"[gpu]   max |log p diff| {err_lp:.3g}, max |attention diff| {err_att:.3g}")
+    assert err_lp < LOGIT_TOL and err_lp < 1e-4
+    assert err_att < 1e-4
+
+
+def test_full_forward_logits_batch(full):
+    """The batched all-row forward (two prompts of 32 + 100 text ids, one with prior codes)
+    against the oracle's per-prompt all-row logits."""
+    W, g, M = full
+    say("[gpu] full forward_logits, batch of 2")
+    prompts, refs = [], []
+    for b in range(2):
+        pr = synth.make_prompt(W.cfg, 32, 100, seed=40 + b)
+        prior = np.arange(b * 20, dtype=np.int32)
+        prompts.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, prior))
+        emb = M.sequence_embedding(pr.text_tokens, pr.conds, pr.lang_id, prior)
+        refs.append(M.forward_rows(M.kv(2048, kv_bf16=False), emb, 0))
+    got = g.forward_logits(prompts)
+    ref = np.concatenate(refs)
+    err = float(np.abs(got - ref).max())
+    say(f"[gpu]   rows {got.shape[0]}, max |logit diff| {err:.3g}")
+    assert got.shape == ref.shape and err < 1e-4
