@@ -214,7 +214,8 @@ itts_status itts_gpt_set_alignment_heads(itts_gpt *gpt, const int32_t *layer_hea
 /* One causal forward of a batch of prompts (each: conds, text, lang, prior codes as in
  * prefill_after) producing the logits of every row of every prompt: logits_out
  * [sum_b T_b][mel_vocab], prompts in order, T_b = n_cond + n_text + 3 + n_prior.  Rows of
- * different prompts do not attend to each other; no cache is read or written.  This is
+ * different prompts do not attend to each other; no cache is read or written.  With
+ * logits_out NULL the logits stay on the device (for timing the forward alone).  This is
  * the multi-row contraction that replay scores with, batched (no reference counterpart
  * beyond teacher_forced's all-row logits, gpt.rs:838-846). */
 itts_status itts_gpt_forward_logits(itts_gpt *gpt, const itts_code_prompt *prompts, int32_t batch,

@@ -71,10 +71,6 @@ hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, in
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,
                               int kvt, hipStream_t s);
 
-// Causal attention of T rows at cache positions base..base+T-1 (prefill); the output
-// rows [T][d] are written in the GEMM's split form.
-hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
-                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s);
 
 // Row descriptors for the prefill embedding.
 struct EmbedRow {
@@ -98,10 +94,19 @@ struct AttnProbe {
   int head, q0, k0, k1;
   float *out;
 };
-// Causal attention of M concatenated rows: row t attends to keys kstart[t]..t of the
-// K/V [n_head][M][64]; the output rows are written in the GEMM's split form.
-hipError_t launch_attn_rows(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
-                            const SplitOut &out, const AttnProbe &p0, const AttnProbe &p1, int kvt, hipStream_t s);
+// Probe of M concatenated rows (row t attends to keys kstart[t]..t of the K/V
+// [n_head][M][64]): writes only the probabilities, for rows p.q0..M-1.
+hipError_t launch_attn_probe(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
+                             const AttnProbe &p, int kvt, hipStream_t s);
+// Causal attention of T rows at cache positions base..base+T-1, one 64-lane block per
+// (head, row) (short prompts); the output rows are written in the GEMM's split form.
+hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
+                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s);
+// Causal attention of T rows on the MFMA units: row t sits at position base + t of the
+// K/V [n_head][ld][64] (bf16 or fp32) and attends to keys ks(t)..base + t, ks(t) =
+// kstart[t] or 0; output rows in the GEMM's split form.
+hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart, const void *kc, const void *vc,
+                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s);
 // out[r] = log_softmax(logits[r])[codes[r]] for R rows of V logits.
 hipError_t launch_log_softmax_pick(const float *logits, int R, int V, const int *codes, float *out, hipStream_t s);
 

@@ -1,0 +1,265 @@
+// Causal multi-row attention on the MFMA units (prefill, replay, all-row forward).
+//
+// Block: two waves, 64 query rows of one head (wave w owns rows 32w..32w+31 in the MFMA
+// output layout).  Keys are processed in tiles of 64: the K rows and the transposed V
+// rows of a tile are read from the cache (bf16 or fp32 [n_head][ld][64]) and split into
+// fp16 hi/lo planes as they are staged in LDS, so that
+//   S = Q K^T = Qh Kh + Qh Kl + Ql Kh      and      O += P V = Ph Vh + Ph Vl + Pl Vh
+// run on v_mfma_f32_32x32x16_f16 with ~22-bit operands and fp32 accumulation.  The
+// softmax is online (running row max and denominator in registers); P goes through a
+// per-wave LDS tile to reach the operand layout of the second product.  16-byte LDS
+// chunks are XOR-swizzled by row so that fragment reads spread over the banks.
+//
+// Query row t sits at cache position base + t and attends to keys ks(t)..base + t, with
+// ks(t) = kstart[t] (concatenated sequences) or 0.
+#include "kernels.h"
+
+namespace itts {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFQ = 64;  // query rows per block
+constexpr int kFK = 64;  // keys per tile
+
+struct FlashLds {
+  uint16_t k[2][kFK * 64];      // [plane][key][dim]
+  uint16_t vt[2][64 * kFK];     // [plane][dim][key]
+  uint16_t p[2][2][32 * kFK];   // [wave][plane][row][key]
+};
+
+// element offset of 16-byte chunk `chunk` of row `row` in a [row][64] fp16 array
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (row & 7)) << 3); }
+
+template <int KVT>
+__device__ __forceinline__ void load8(const void *base, size_t idx, float v[8]) {
+  if constexpr (KVT == kKvBf16) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + idx);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      v[2 * j] = __uint_as_float(w[j] << 16);
+      v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx);
+    const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(base) + idx + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+}
+
+__device__ __forceinline__ void split8(const float v[8], u32x4 &hi, u32x4 &lo) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint32_t h0, l0, h1, l1;
+    split_f16(v[2 * j], h0, l0);
+    split_f16(v[2 * j + 1], h1, l1);
+    hi[j] = h0 | (h1 << 16);
+    lo[j] = l0 | (l1 << 16);
+  }
+}
+
+__device__ __forceinline__ float half_max32(float v) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float half_sum32(float v) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+#define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
+
+template <int KVT>
+__global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, const void *kc, const void *vc,
+                                                         int ld, int base, int T, const int *kstart, SplitOut out) {
+  __shared__ FlashLds sh;
+  const int h = blockIdx.x, q0 = blockIdx.y * kFQ;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const size_t hb = (size_t)h * ld * 64;
+  const void *kh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(kc) + hb)
+                                  : (const void *)(static_cast<const float *>(kc) + hb);
+  const void *vh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(vc) + hb)
+                                  : (const void *)(static_cast<const float *>(vc) + hb);
+
+  // Q fragments of this lane's row (operand layout: row lane & 31, dims kk*16 + (lane>>5)*8 ..)
+  f16x8 qh[4], ql[4];
+  {
+    const int t = min(q0 + w * 32 + (lane & 31), T - 1);
+    const float *qp = q + (size_t)t * d + h * 64 + (lane >> 5) * 8;
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      float v[8];
+      const float4 a = *reinterpret_cast<const float4 *>(qp + kk * 16);
+      const float4 b = *reinterpret_cast<const float4 *>(qp + kk * 16 + 4);
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+      u32x4 hi, lo;
+      split8(v, hi, lo);
+      qh[kk] = __builtin_bit_cast(f16x8, hi);
+      ql[kk] = __builtin_bit_cast(f16x8, lo);
+    }
+  }
+  // output-layout rows of this lane: r(i) = (i>>2)*8 + (lane>>5)*4 + (i&3)
+  int pos[16], ks[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+    pos[i] = base + t;
+    ks[i] = kstart ? kstart[min(t, T - 1)] : 0;
+  }
+  float m[16], l[16];
+  floatx16 O[2];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+    O[0][i] = 0.0f;
+    O[1][i] = 0.0f;
+  }
+
+  const int kmin = kstart ? kstart[q0] : 0;
+  const int kmax = base + min(q0 + kFQ - 1, T - 1);
+  for (int kb = (kmin / kFK) * kFK; kb <= kmax; kb += kFK) {
+    __syncthreads();  // the previous tile's operands are no longer read
+    {  // K rows: thread -> key tid/2, dims (tid&1)*32 .. +31
+      const int kr = tid >> 1, key = min(kb + kr, ld - 1);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int chunk = (tid & 1) * 4 + c;
+        float v[8];
+        load8<KVT>(kh, (size_t)key * 64 + chunk * 8, v);
+        u32x4 hi, lo;
+        split8(v, hi, lo);
+        *reinterpret_cast<u32x4 *>(&sh.k[0][swz(kr, chunk)]) = hi;
+        *reinterpret_cast<u32x4 *>(&sh.k[1][swz(kr, chunk)]) = lo;
+      }
+    }
+    {  // V transposed: thread -> keys 2kp, 2kp+1, dims (tid&3)*16 .. +15
+      const int kp = tid >> 2;
+      const int k0 = min(kb + 2 * kp, ld - 1), k1 = min(kb + 2 * kp + 1, ld - 1);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int e0 = (tid & 3) * 16 + c * 8;
+        float a[8], b[8];
+        load8<KVT>(vh, (size_t)k0 * 64 + e0, a);
+        load8<KVT>(vh, (size_t)k1 * 64 + e0, b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int e = e0 + j;
+          uint32_t ha, la, hb2, lb;
+          split_f16(a[j], ha, la);
+          split_f16(b[j], hb2, lb);
+          const int idx = e * 64 + ((((2 * kp) >> 3) ^ (e & 7)) << 3) + ((2 * kp) & 7);
+          *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
+          *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
+        }
+      }
+    }
+    __syncthreads();
+
+    floatx16 S[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) S[kt][i] = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const int o = swz(kt * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        const f16x8 bh = *reinterpret_cast<const f16x8 *>(&sh.k[0][o]);
+        const f16x8 bl = *reinterpret_cast<const f16x8 *>(&sh.k[1][o]);
+        S[kt] = MFMA16(qh[kk], bh, S[kt], 0, 0, 0);
+        S[kt] = MFMA16(qh[kk], bl, S[kt], 0, 0, 0);
+        S[kt] = MFMA16(ql[kk], bh, S[kt], 0, 0, 0);
+      }
+    }
+
+    uint16_t *pw = sh.p[w][0];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        const int key = kb + kt * 32 + (lane & 31);
+        s[kt] = (key > pos[i] || key < ks[i]) ? -INFINITY : S[kt][i] * 0.125f;
+      }
+      const float mn = fmaxf(m[i], half_max32(fmaxf(s[0], s[1])));
+      const float corr = m[i] == -INFINITY ? 1.0f : __expf(m[i] - mn);
+      const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      float psum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        const float p = s[kt] == -INFINITY ? 0.0f : __expf(s[kt] - mn);
+        psum += p;
+        uint32_t ph, pl;
+        split_f16(p, ph, pl);
+        const int key = kt * 32 + (lane & 31);
+        const int o = r * 64 + (((key >> 3) ^ (r & 7)) << 3) + (key & 7);
+        pw[o] = (uint16_t)ph;
+        pw[32 * kFK + o] = (uint16_t)pl;
+      }
+      l[i] = l[i] * corr + psum;
+      O[0][i] *= corr;
+      O[1][i] *= corr;
+      m[i] = mn;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's P tile is in LDS
+
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const int oa = swz(lane & 31, kk * 2 + (lane >> 5));
+      const f16x8 ah = *reinterpret_cast<const f16x8 *>(&pw[oa]);
+      const f16x8 al = *reinterpret_cast<const f16x8 *>(&pw[32 * kFK + oa]);
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++) {
+        const int ob = swz(dt * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        const f16x8 bh = *reinterpret_cast<const f16x8 *>(&sh.vt[0][ob]);
+        const f16x8 bl = *reinterpret_cast<const f16x8 *>(&sh.vt[1][ob]);
+        O[dt] = MFMA16(ah, bh, O[dt], 0, 0, 0);
+        O[dt] = MFMA16(ah, bl, O[dt], 0, 0, 0);
+        O[dt] = MFMA16(al, bh, O[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // normalise and write the rows in the GEMM's split form (one head = one 64-group)
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+    const float inv = 1.0f / half_sum32(l[i]);
+    const float v0 = O[0][i] * inv, v1 = O[1][i] * inv;
+    const float gsum = half_sum32(v0 + v1);
+    if (t < T) {
+      const size_t row = (size_t)t * d + h * 64 + (lane & 31);
+      uint32_t hi, lo;
+      split_f16(v0, hi, lo);
+      out.hi[row] = (uint16_t)hi;
+      out.lo[row] = (uint16_t)lo;
+      split_f16(v1, hi, lo);
+      out.hi[row + 32] = (uint16_t)hi;
+      out.lo[row + 32] = (uint16_t)lo;
+      if ((lane & 31) == 0) out.gs[(size_t)t * (d / 64) + h] = gsum;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart, const void *kc, const void *vc,
+                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s) {
+  if (T <= 0 || base + T > ld) return hipErrorInvalidValue;
+  dim3 grid(n_head, (T + kFQ - 1) / kFQ);
+  const int d = n_head * 64;
+  if (kvt == kKvBf16) {
+    hipLaunchKernelGGL(attn_flash_kernel<kKvBf16>, grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart, out);
+  } else {
+    hipLaunchKernelGGL(attn_flash_kernel<kKvF32>, grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart, out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace itts

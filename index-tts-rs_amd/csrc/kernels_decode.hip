@@ -494,40 +494,35 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int ba
   put_split(out, (size_t)t * d + h * 64 + threadIdx.x, (size_t)t * (d / 64) + h, o / l);
 }
 
-// Attention over concatenated sequences (replay / all-row logits): row t attends to the
-// keys kstart[t]..t of the scratch K/V [n_head][ld][64]; up to two probes export the
-// softmax probabilities of one head for the queries q0.. over the key columns [k0, k1).
+// Attention probe (replay, gpt.rs:391-422): softmax probabilities of head p.head for the
+// query rows p.q0.. over the key columns [p.k0, p.k1) of the K/V [n_head][ld][64]; row t
+// attends to keys kstart[t]..t.  One block per query row; the attention output itself is
+// produced by the flash kernel.
 template <int KVT>
-__global__ __launch_bounds__(64) void attn_rows_kernel(const float *q, const void *kc, const void *vc, int ld,
-                                                       const int *kstart, int d, SplitOut out, AttnProbe p0,
-                                                       AttnProbe p1) {
+__global__ __launch_bounds__(64) void attn_probe_kernel(const float *q, const void *kc, const void *vc, int ld,
+                                                        const int *kstart, int d, AttnProbe pr) {
   __shared__ float p_lds[64];
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const int h = pr.head, t = pr.q0 + blockIdx.x, lane = threadIdx.x;
   const size_t hb = (size_t)h * ld * 64;
   const int j0 = kstart[t];
   const void *kh = head_base<KVT>(kc, hb);
   const float *qt = q + (size_t)t * d + h * 64;
   float m, l, o;
   attn_range<KVT>(qt, kh, head_base<KVT>(vc, hb), j0, t + 1, m, l, o, p_lds);
-  put_split(out, (size_t)t * d + h * 64 + lane, (size_t)t * (d / 64) + h, o / l);
-  for (int pi = 0; pi < 2; pi++) {
-    const AttnProbe &pr = pi == 0 ? p0 : p1;
-    if (pr.head != h || t < pr.q0) continue;
-    const int w = pr.k1 - pr.k0;
-    for (int c0 = 0; c0 < w; c0 += 64) {
-      const int c = c0 + lane, j = pr.k0 + c;
-      if (c >= w) continue;
-      float p = 0.0f;
-      if (j >= j0 && j <= t) {  // the score exactly as attn_range formed it
-        float kr[64];
-        load_row64<KVT>(kh, (size_t)j, kr);
-        float dot = 0.0f;
+  const int w = pr.k1 - pr.k0;
+  for (int c0 = 0; c0 < w; c0 += 64) {
+    const int c = c0 + lane, j = pr.k0 + c;
+    if (c >= w) continue;
+    float p = 0.0f;
+    if (j >= j0 && j <= t) {  // the score exactly as attn_range formed it
+      float kr[64];
+      load_row64<KVT>(kh, (size_t)j, kr);
+      float dot = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 64; e++) dot += qt[e] * kr[e];
-        p = __expf(dot * 0.125f - m) / l;
-      }
-      pr.out[(size_t)(t - pr.q0) * w + c] = p;
+      for (int e = 0; e < 64; e++) dot += qt[e] * kr[e];
+      p = __expf(dot * 0.125f - m) / l;
     }
+    pr.out[(size_t)(t - pr.q0) * w + c] = p;
   }
 }
 
@@ -623,17 +618,6 @@ hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, in
   return hipGetLastError();
 }
 
-hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
-                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
-  dim3 grid(n_head, T);
-  const int d = n_head * 64;
-  if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvBf16>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
-  } else {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvF32>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
-  }
-  return hipGetLastError();
-}
 
 hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
                              const float *text_emb, const float *lang_row,
@@ -651,14 +635,27 @@ hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T,
   return hipGetLastError();
 }
 
-hipError_t launch_attn_rows(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
-                            const SplitOut &out, const AttnProbe &p0, const AttnProbe &p1, int kvt, hipStream_t s) {
-  dim3 grid(n_head, M);
+hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
+                               int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
+  dim3 grid(n_head, T);
   const int d = n_head * 64;
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_rows_kernel<kKvBf16>, grid, dim3(64), 0, s, q, kc, vc, M, kstart, d, out, p0, p1);
+    hipLaunchKernelGGL(attn_prefill_kernel<kKvBf16>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
   } else {
-    hipLaunchKernelGGL(attn_rows_kernel<kKvF32>, grid, dim3(64), 0, s, q, kc, vc, M, kstart, d, out, p0, p1);
+    hipLaunchKernelGGL(attn_prefill_kernel<kKvF32>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_probe(const float *q, int M, const int *kstart, const void *kc, const void *vc, int n_head,
+                             const AttnProbe &p, int kvt, hipStream_t s) {
+  if (p.head < 0 || p.head >= n_head || p.q0 < 0 || p.q0 >= M || p.k0 < 0 || p.k1 <= p.k0 || !p.out)
+    return hipErrorInvalidValue;
+  const int d = n_head * 64;
+  if (kvt == kKvBf16) {
+    hipLaunchKernelGGL(attn_probe_kernel<kKvBf16>, dim3(M - p.q0), dim3(64), 0, s, q, kc, vc, M, kstart, d, p);
+  } else {
+    hipLaunchKernelGGL(attn_probe_kernel<kKvF32>, dim3(M - p.q0), dim3(64), 0, s, q, kc, vc, M, kstart, d, p);
   }
   return hipGetLastError();
 }

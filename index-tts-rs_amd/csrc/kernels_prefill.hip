@@ -65,6 +65,9 @@ __device__ __forceinline__ uint32_t f16_pair_u4(uint32_t w, int sh) {
 // compiler cannot tell which ring buffer a pending copy targets, so the builtin makes it
 // wait for every copy in flight before any LDS read; issued here, the copies are counted
 // by the kernel's own vmcnt waits instead.
+// M0 is reserved to the compiler; these kernels use it for nothing else (the copies set
+// it themselves before every copy), so the clobber warning is expected.
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(lds_ptr)(p);
 }

@@ -259,6 +259,10 @@ DevSampling to_dev_sampling(const itts_sampling &p, int n) {
   return d;
 }
 
+// Prompts up to this many rows use the per-row attention kernel, longer ones the MFMA
+// flash kernel (measured crossover on MI355X at 24 layers x 20 heads).
+constexpr int kFlashMinRows = 384;
+
 // GEMM arguments over M rows with the decoder's split-K workspace.
 GemmArgs gemm_args(const itts_gpt *g, const DevQL &ql, SplitAct x, int M) {
   GemmArgs ga{};
@@ -357,8 +361,13 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
     GemmArgs ga = gemm(L.attn, g->ph.act());
     ga.qkv = QkvDst{Q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kv->kvt, s));
-    HIP_TRY(launch_attn_prefill(Q, T, 0, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, g->pa.out(),
-                                kv->kvt, s));
+    if (T <= kFlashMinRows) {  // few query tiles: one block per (head, row) spreads wider
+      HIP_TRY(launch_attn_prefill(Q, T, 0, kv->k_layer(l), kv->v_layer(l), c.n_head, kv->max_seq, g->pa.out(),
+                                  kv->kvt, s));
+    } else {
+      HIP_TRY(launch_attn_flash(Q, T, 0, nullptr, kv->k_layer(l), kv->v_layer(l), kv->max_seq, c.n_head,
+                                g->pa.out(), kv->kvt, s));
+    }
     ga = gemm(L.proj, g->pa.act());
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
@@ -520,12 +529,11 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
     GemmArgs ga = gemm_args(g, L.attn, g->ph.act(), M);
     ga.qkv = QkvDst{Q, g->rk.p, g->rv.p, M, 0, d};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kKvF32, s));
-    AttnProbe pr[2] = {{-1, 0, 0, 0, nullptr}, {-1, 0, 0, 0, nullptr}};
-    int np = 0;
-    for (const ProbeSpec &p : probes)
-      if (p.layer == l && np < 2) pr[np++] = AttnProbe{p.head, p.q0, p.k0, p.k1, p.out};
-    HIP_TRY(launch_attn_rows(Q, M, g->kstart.as<int>(), g->rk.p, g->rv.p, c.n_head, g->pa.out(), pr[0], pr[1],
-                             kKvF32, s));
+    for (const ProbeSpec &p : probes)  // read-only exports of this layer's attention
+      if (p.layer == l)
+        HIP_TRY(launch_attn_probe(Q, M, g->kstart.as<int>(), g->rk.p, g->rv.p, c.n_head,
+                                  AttnProbe{p.head, p.q0, p.k0, p.k1, p.out}, kKvF32, s));
+    HIP_TRY(launch_attn_flash(Q, M, 0, g->kstart.as<int>(), g->rk.p, g->rv.p, M, c.n_head, g->pa.out(), kKvF32, s));
     ga = gemm_args(g, L.proj, g->pa.act(), M);
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
@@ -1052,8 +1060,8 @@ itts_status itts_gpt_set_alignment_heads(itts_gpt *gpt, const int32_t *pairs, in
 
 itts_status itts_gpt_forward_logits(itts_gpt *gpt, const itts_code_prompt *prompts, int32_t batch,
                                     float *logits_out) {
-  if (!gpt || !prompts || batch <= 0 || !logits_out)
-    return set_error(ITTS_E_VALIDATION, "prompts: a non-empty batch and an output are required");
+  if (!gpt || !prompts || batch <= 0)
+    return set_error(ITTS_E_VALIDATION, "prompts: a non-empty batch is required");
   std::vector<int> row0, T;
   int M = 0;
   if (itts_status st = embed_prompts(gpt, prompts, batch, row0, T, &M)) return st;
@@ -1062,8 +1070,9 @@ itts_status itts_gpt_forward_logits(itts_gpt *gpt, const itts_code_prompt *promp
     for (int r = 0; r < T[b]; r++) kstart[row0[b] + r] = row0[b];
   if (itts_status st = forward_rows_stack(gpt, M, kstart, gpt->cfg.n_layer, {})) return st;
   if (itts_status st = head_rows(gpt, 0, M)) return st;
-  HIP_TRY(hipMemcpyAsync(logits_out, gpt->plog.p, sizeof(float) * (size_t)M * gpt->cfg.mel_vocab,
-                         hipMemcpyDeviceToHost, gpt->stream));
+  if (logits_out)
+    HIP_TRY(hipMemcpyAsync(logits_out, gpt->plog.p, sizeof(float) * (size_t)M * gpt->cfg.mel_vocab,
+                           hipMemcpyDeviceToHost, gpt->stream));
   HIP_TRY(hipStreamSynchronize(gpt->stream));
   return ITTS_OK;
 }

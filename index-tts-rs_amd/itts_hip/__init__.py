@@ -368,8 +368,9 @@ class Gpt:
         a = np.ascontiguousarray(np.asarray(pairs, dtype=np.int32).reshape(-1))
         _check(lib.itts_gpt_set_alignment_heads(self._h, _ptr(a), len(a) // 2))
 
-    def forward_logits(self, prompts):
-        """All-row logits of a batch of CodePrompts in one forward: [sum T_b][mel_vocab]."""
+    def forward_logits(self, prompts, copy_out=True):
+        """All-row logits of a batch of CodePrompts in one forward: [sum T_b][mel_vocab]
+        (copy_out=False leaves them on the device and returns None)."""
         keep, arr = [], (itts_code_prompt * len(prompts))()
         rows = 0
         for i, p in enumerate(prompts):
@@ -378,7 +379,7 @@ class Gpt:
             keep += [t, c, pr]
             arr[i] = itts_code_prompt(_ptr(t), len(t), _ptr(c), c.shape[0], int(p.lang_id), _ptr(pr), len(pr), 0)
             rows += c.shape[0] + len(t) + 3 + len(pr)
-        out = np.empty((rows, self.cfg["mel_vocab"]), np.float32)
+        out = np.empty((rows, self.cfg["mel_vocab"]), np.float32) if copy_out else None
         _check(lib.itts_gpt_forward_logits(self._h, C.cast(arr, C.c_void_p), len(prompts), _ptr(out)))
         return out
 

@@ -35,7 +35,7 @@ def full():
     g.close()
 
 
-@pytest.mark.parametrize("n_cond,n_text", [(32, 64), (32, 200)])
+@pytest.mark.parametrize("n_cond,n_text", [(32, 64), (32, 200), (32, 500)])
 def test_full_prefill_logits(full, n_cond, n_text):
     W, g, M = full
     say(f"[gpu] full prefill {n_cond}+{n_text}")

@@ -134,3 +134,24 @@ def test_replay_validation(tiny):
         assert lp.shape == (2,)
     finally:
         g2.close()
+
+
+@pytest.mark.parametrize("kvt", [H.ITTS_BF16, H.ITTS_F32])
+def test_long_prefill_flash_attention_matches_oracle(tiny, kvt):
+    """Prompts above 384 rows take the MFMA flash attention in prefill (cache K/V read as
+    bf16 or fp32): logits and the cache match the oracle, and decode continues from it."""
+    W, g, M = tiny
+    say(f"[gpu] long prefill (flash attention) kv={kvt}")
+    pr = synth.make_prompt(W.cfg, 3, 100, seed=77)
+    prior = np.random.default_rng(7).integers(0, 1000, 450).astype(np.int32)
+    kv = g.kv_cache(1024, kvt)
+    okv = M.kv(1024, kv_bf16=kvt == H.ITTS_BF16)
+    a = g.prefill_after(pr.text_tokens, pr.conds, pr.lang_id, prior, kv)
+    b = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id, prior)
+    assert kv.valid_len() == okv.valid_len() == 3 + 100 + 3 + 450
+    tol = TIGHT if kvt == H.ITTS_F32 else 2e-3
+    assert np.abs(a - b).max() < tol
+    for t in (5, 17):
+        a = g.step(kv, t, 452 + t)
+        b = M.step(okv, t, 452 + t)
+        assert np.abs(a - b).max() < tol
