@@ -13,6 +13,9 @@ replay of the captured sample+step graph) is the unit whose HBM roofline is repo
 achieved = algorithmic bytes of one decode step / its average device time (HIP events
 on the decoder's stream).
 
+The default run also reports, under "secondary", the prefill-heavy workload (4 x 547
+rows, all-row logits, MFMA-bound) and the int4 decode workload.
+
 Usage: python bench.py [--steps K] [--warmup W] [--workload long|short|int4]
 """
 import argparse
@@ -110,6 +113,61 @@ def measured_traffic(decode_path):
         return None
 
 
+def prefill_heavy(H, synth, g, cfg, seed):
+    """The prefill-heavy workload: 4 prompts of 32 cond + 512 text ids (4 x 547 = 2188 rows)
+    in one causal forward producing the logits of every row (kept on the device); median of
+    3 calls after one warm-up, host call to return.  FLOPs are the algorithmic ones: the
+    linears of every row (24 blocks + mel_head) and causal attention."""
+    prompts = []
+    for b in range(4):
+        pr = synth.make_prompt(cfg, 32, 512, seed=seed + 10 + b)
+        prompts.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None))
+    g.forward_logits(prompts, copy_out=False)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        g.forward_logits(prompts, copy_out=False)
+        times.append((time.perf_counter() - t0) * 1e3)
+    ms = statistics.median(times)
+    d, F, V, L, rows, T = 1280, 5120, 8194, 24, 4 * 547, 547
+    lin = 2.0 * rows * (L * (d * 3 * d + d * d + d * F + F * d) + d * V)
+    att = 4 * L * 20 * (T * (T + 1) / 2) * 64 * 2 * 2
+    tflop = (lin + att) / 1e12
+    print(f"[bench] prefill-heavy forward: {ms:.2f} ms", file=sys.stderr, flush=True)
+    return {"workload": "batch 4 x (32 cond + 512 text) = 2188 rows, one forward, logits of all rows",
+            "ms": round(ms, 3), "tflop": round(tflop, 4), "achieved_tflops": round(tflop / (ms * 1e-3), 1),
+            "bound": "mfma", "peak_tflops": 2500.0,
+            "frac": round(tflop / (ms * 1e-3) / 2500.0, 4),
+            "note": "fp16 MFMA with hi/lo split activations (two products per weight)"}
+
+
+def int4_decode(H, synth, seed):
+    """The int4 workload: 4-bit weights, prefill 32 + 128 text (163 rows), 1500 greedy
+    steps with STOP masked; device-timed decode rate and the HBM roofline of one step."""
+    n_cond, n_text, n_steps, samp, bits, desc = WORKLOADS["int4"]
+    cfg = dict(synth.FULL_CONFIG, quant_bits=bits)
+    W = synth.make_weights(cfg, seed=seed)
+    wb = W.weight_bytes_per_step()
+    g = H.Gpt(W)
+    kv = g.kv_cache(2048, H.ITTS_BF16)
+    path = "persistent" if kv.decode_path() == H.ITTS_DECODE_PERSISTENT else "multi-kernel"
+    prompt = synth.make_prompt(cfg, n_cond, n_text, seed=seed + 1)
+    sp = H.SamplingParams(max_mel_tokens=n_steps, **samp)
+    cp = H.CodePrompt(prompt.text_tokens, prompt.conds, prompt.lang_id, None, n_steps)
+    H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(1))
+    codes = H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(1))
+    t = kv.last_timing()
+    step_ms = t["decode_ms"] / t["decode_steps"]
+    mean_L = t["prefill_rows"] + (t["decode_steps"] + 1) / 2.0
+    achieved = step_bytes(wb, int(round(mean_L))) / (step_ms * 1e-3) / 1e9
+    print(f"[bench] int4 decode: {1e3 / step_ms:.1f} tokens/s ({path})", file=sys.stderr, flush=True)
+    g.close()
+    return {"workload": desc, "decode_path": path, "tokens": int(len(codes)),
+            "decode_tokens_per_s": round(1e3 / step_ms, 2), "decode_step_us": round(step_ms * 1e3, 2),
+            "prefill_ms": round(t["prefill_ms"], 3), "weight_bytes_per_step": wb,
+            "hbm_achieved_gbs": round(achieved, 1), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,6 +176,8 @@ def main():
     ap.add_argument("--workload", default="long", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the prefill-heavy (4 x 547 rows) and int4 decode measurements")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--decode", default="auto", choices=["auto", "multi", "persistent"],
                     help="decode-step implementation (auto: persistent where supported)")
@@ -232,6 +292,10 @@ def main():
                      "traffic": traffic, "kernel": kernel_name,
                      "bytes_per_launch": bytes_step, "mean_keys": mean_L},
     }
+    if not args.no_secondary and args.workload == "long":
+        out["secondary"] = {"prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed)}
+        del g, kv
+        out["secondary"]["int4_decode"] = int4_decode(H, synth, args.seed)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(W, prompt, sp, args.cpu_steps)
