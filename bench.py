@@ -178,6 +178,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill-heavy (4 x 547 rows) and int4 decode measurements")
+    ap.add_argument("--only", choices=["prefill", "prefill-heavy"],
+                    help="for profilers: only repeat the workload's prefill or the prefill-heavy "
+                         "forward --repeat times, print one line per call, no JSON")
+    ap.add_argument("--repeat", type=int, default=6)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--decode", default="auto", choices=["auto", "multi", "persistent"],
                     help="decode-step implementation (auto: persistent where supported)")
@@ -199,6 +203,21 @@ def main():
     print(f"[bench] weights generated in {time.perf_counter() - t0:.1f}s "
           f"({weight_bytes / 1e6:.1f} MB per decode step)", file=sys.stderr, flush=True)
     g = H.Gpt(W)
+    if args.only:
+        prompt = synth.make_prompt(cfg, n_cond, n_text, seed=args.seed + 1)
+        kv = g.kv_cache(2048, H.ITTS_BF16)
+        heavy = []
+        for b in range(4):
+            pr = synth.make_prompt(cfg, 32, 512, seed=args.seed + 10 + b)
+            heavy.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None))
+        for i in range(args.repeat):
+            t0 = time.perf_counter()
+            if args.only == "prefill":
+                g.prefill(prompt.text_tokens, prompt.conds, prompt.lang_id, kv, logits=False)
+            else:
+                g.forward_logits(heavy, copy_out=False)
+            print(f"[bench] {args.only} call {i}: {(time.perf_counter() - t0) * 1e3:.2f} ms", flush=True)
+        return
     g.set_decode_path({"auto": H.ITTS_DECODE_AUTO, "multi": H.ITTS_DECODE_MULTI,
                        "persistent": H.ITTS_DECODE_PERSISTENT}[args.decode])
     kv = g.kv_cache(2048, H.ITTS_BF16)
