@@ -241,6 +241,23 @@ itts_status itts_sample_next_token(itts_gpt *gpt, float *logits, int32_t n,
 itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_code_prompt *prompt,
                                       const itts_sampling *p, uint64_t *rng_state,
                                       int32_t *codes_out, int32_t codes_cap, int32_t *n_codes);
+/* ---- batched decode (independent sequences stepped together) ---- */
+/* One Gpt::step for each of `batch` sequences (tokens[b] at positions[b] on caches[b]),
+ * computed together: every weight byte is read once for the whole batch.  Caches must be
+ * distinct, of this decoder, and of one capacity and dtype.  logits_out receives
+ * [batch][mel_vocab] (may be NULL).  Per sequence the result is Gpt::step's. */
+itts_status itts_gpt_step_batch(itts_gpt *gpt, itts_kv *const *caches, int32_t batch,
+                                const int32_t *tokens, const int32_t *positions, float *logits_out);
+/* generate_codes_after for `batch` sequences at once: each prompt is prefilled into its
+ * cache, then the sequences are sampled and stepped together (one batched step per token)
+ * until every one has stopped (STOP after its min_codes, or its max steps); a finished
+ * sequence's row is carried but does nothing.  params and rng_states are per sequence;
+ * codes_out is [batch][codes_cap] and n_codes [batch].  Per sequence, the codes and the
+ * final RNG state equal generate_codes_after on that sequence alone. */
+itts_status itts_generate_codes_batch(itts_gpt *gpt, itts_kv *const *caches, const itts_code_prompt *prompts,
+                                      const itts_sampling *params, int32_t batch, uint64_t *rng_states,
+                                      int32_t *codes_out, int32_t codes_cap, int32_t *n_codes);
+
 /* Device-side timing of the last generate call on this cache, from HIP events recorded
  * on the decoder's stream (the counterpart of the reference's StageTimings.gpt_ms,
  * crates/core/src/engine/stream.rs:19-44, split into its two phases). */

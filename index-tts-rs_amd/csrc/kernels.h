@@ -34,8 +34,18 @@ struct SplitOut {
   SplitAct act() const { return SplitAct{hi, lo, gs}; }
 };
 
+// One sequence of a batched decode step: its control block, its cache bases (layer 0 of
+// [layer][n_head][max_seq][64]) and its code output.
+struct BatchSeq {
+  DecodeCtl *ctl;
+  void *k, *v;
+  int32_t *codes;
+};
+
 // Where the QKV epilogue scatters: q -> q_out[M][d]; k, v -> this layer's cache
-// [n_head][max_seq][64] at rows pos0.. (pos0 = ctl->valid_len when ctl != nullptr).
+// [n_head][max_seq][64] at rows pos0.. .  With seqs set (batched decode), row m belongs
+// to sequence m: its K/V row goes to seqs[m]'s cache at offset layer_off (elements) and
+// position ctl->valid_len, and nothing is written for a finished sequence.
 struct QkvDst {
   float *q_out;
   void *k_cache;
@@ -43,6 +53,8 @@ struct QkvDst {
   int max_seq;
   int pos0;
   int d_model;
+  const BatchSeq *seqs;
+  size_t layer_off;
 };
 
 struct GemvArgs {
@@ -67,6 +79,15 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
 // 64 unnormalised outputs) to part [n_head][max_splits][66]; the consumer (the c_proj
 // GEMV's kProAttn prologue) combines them.
 int attn_decode_max_splits(int max_seq);
+// Batched decode attention (grid head x split x sequence) and the split combine into the
+// sequences' attention rows [B][d] in split form; finished sequences are skipped.
+hipError_t launch_decode_batch_parts(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
+                                     int max_seq, float *part, const SplitOut &out, int kvt, hipStream_t s);
+// x[b] = mel_emb[tok_b] + mel_pos[pos_b] from the sequences' control blocks.
+hipError_t launch_embed_batch(const BatchSeq *seqs, int B, const float *mel_emb, const float *mel_pos, int d, float *x,
+                              hipStream_t s);
+// valid_len += 1 for every sequence that is not finished.
+hipError_t launch_advance_batch(const BatchSeq *seqs, int B, hipStream_t s);
 hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, int n_head,
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,
                               int kvt, hipStream_t s);
@@ -127,6 +148,8 @@ struct GemmArgs {
   int n_cu;         // compute units (grid sizing)
 };
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s);
+// Sets the LDS attributes of every GEMM instantiation (before any graph capture).
+hipError_t gemm_init();
 size_t gemm_ws_floats(int n_cu);
 constexpr int kGemmCounters = 4096;
 
@@ -180,5 +203,10 @@ hipError_t sampler_init();
 hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSampling p,
                           uint64_t *rng, int32_t *tok_out, DecodeCtl *ctl, int32_t *codes,
                           int stop_tok, int mode, hipStream_t s);
+// One sampler block per sequence of a batch: block b samples logits[b][n] with ps[b] into
+// seqs[b]'s control block and codes (the generate loop's mode).  lds_top_k is the largest
+// top_k of the batch (sets the LDS of the candidate sort).
+hipError_t launch_sampler_batch(float *logits, int n, const DevSampling *ps, const BatchSeq *seqs, int B,
+                                int stop_tok, int lds_top_k, bool any_sampled, hipStream_t s);
 
 }  // namespace itts

@@ -330,13 +330,11 @@ struct AttnShared {
   float m[4], l[4];
 };
 
+// One block of the decode attention: head h, key split s of the n_splits splits.
 template <int KVT>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const void *kc, const void *vc,
-                                                          int max_seq, const DecodeCtl *ctl, int static_len,
-                                                          float *part) {
-  if (ctl != nullptr && ctl->done) return;
-  __shared__ AttnShared sh;
-  const int h = blockIdx.x, s = blockIdx.y;
+__device__ inline void attn_decode_block(const float *q, const void *kc, const void *vc, int max_seq,
+                                         const DecodeCtl *ctl, int static_len, float *part, int h, int s,
+                                         int n_splits, AttnShared &sh) {
   const int L = ctl != nullptr ? ctl->valid_len + 1 : static_len;
   const int S = (L + kAttnKeys - 1) / kAttnKeys;  // active splits
   if (s >= S) return;
@@ -403,7 +401,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
   __syncthreads();
   // block partial: the four waves merged
   if (wave == 0) {
-    float *mine = part + ((size_t)h * gridDim.y + s) * 66;
+    float *mine = part + ((size_t)h * n_splits + s) * 66;
     float M = -INFINITY;
     for (int w = 0; w < 4; w++) M = fmaxf(M, sh.m[w]);
     float lsum = 0.0f, osum = 0.0f;
@@ -419,6 +417,77 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
       mine[1] = lsum;
     }
   }
+}
+
+template <int KVT>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const void *kc, const void *vc,
+                                                          int max_seq, const DecodeCtl *ctl, int static_len,
+                                                          float *part) {
+  if (ctl != nullptr && ctl->done) return;
+  __shared__ AttnShared sh;
+  attn_decode_block<KVT>(q, kc, vc, max_seq, ctl, static_len, part, blockIdx.x, blockIdx.y, gridDim.y, sh);
+}
+
+// Batched decode attention: grid (head, split, sequence); sequence b reads its query row
+// q[b], its cache (layer offset layer_off from its base) and its length from its control
+// block, and writes its partials at part + b * n_head * n_splits * 66.
+template <int KVT>
+__global__ __launch_bounds__(256) void attn_decode_batch_kernel(const float *q, const BatchSeq *seqs, size_t layer_off,
+                                                                int max_seq, float *part) {
+  const BatchSeq &sq = seqs[blockIdx.z];
+  if (sq.ctl->done) return;
+  __shared__ AttnShared sh;
+  const int H = gridDim.x, d = H * 64;
+  const size_t es = KVT == kKvBf16 ? 2 : 4;
+  const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
+  const void *vc = static_cast<const char *>(sq.v) + layer_off * es;
+  attn_decode_block<KVT>(q + (size_t)blockIdx.z * d, kc, vc, max_seq, sq.ctl, 0,
+                         part + (size_t)blockIdx.z * H * gridDim.y * 66, blockIdx.x, blockIdx.y, gridDim.y, sh);
+}
+
+// Combines the split partials of each (sequence, head) into the attention output row of
+// the sequence, in the GEMM's split form.  Finished sequences leave their row untouched.
+__global__ __launch_bounds__(64) void attn_combine_batch_kernel(const float *part, const BatchSeq *seqs, int n_splits,
+                                                                int d, SplitOut out) {
+  const int b = blockIdx.y, h = blockIdx.x, lane = threadIdx.x;
+  const DecodeCtl *ctl = seqs[b].ctl;
+  if (ctl->done) return;
+  const int H = gridDim.x;
+  const int S = (ctl->valid_len + 1 + kAttnKeys - 1) / kAttnKeys;
+  const float *ph = part + ((size_t)b * H + h) * n_splits * 66;
+  float M = -INFINITY;
+  for (int s = 0; s < S; s++) M = fmaxf(M, ph[s * 66]);
+  float den = 0.0f, num = 0.0f;
+  for (int s = 0; s < S; s++) {
+    const float m = ph[s * 66];
+    if (m == -INFINITY) continue;
+    const float f = __expf(m - M);
+    den += ph[s * 66 + 1] * f;
+    num += ph[s * 66 + 2 + lane] * f;
+  }
+  const float v = num / den;
+  uint32_t hi, lo;
+  split_f16(v, hi, lo);
+  const size_t i = (size_t)b * d + h * 64 + lane;
+  out.hi[i] = (uint16_t)hi;
+  out.lo[i] = (uint16_t)lo;
+  const float gsum = wave_sum(v);
+  if (lane == 0) out.gs[(size_t)b * (d / 64) + h] = gsum;
+}
+
+// Row b of a batched step: mel_emb[tok] + mel_pos[pos] of sequence b (from its control block).
+__global__ __launch_bounds__(256) void embed_batch_kernel(const BatchSeq *seqs, const float *mel_emb,
+                                                          const float *mel_pos, int d, float *x) {
+  const DecodeCtl *ctl = seqs[blockIdx.x].ctl;
+  const float *me = mel_emb + (size_t)ctl->tok * d;
+  const float *mp = mel_pos + (size_t)ctl->pos * d;
+  for (int i = threadIdx.x; i < d; i += 256) x[(size_t)blockIdx.x * d + i] = me[i] + mp[i];
+}
+
+// After a batched step: every running sequence has one more cache row.
+__global__ void advance_batch_kernel(const BatchSeq *seqs, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B && !seqs[b].ctl->done) seqs[b].ctl->valid_len += 1;
 }
 
 // One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows).
@@ -603,6 +672,32 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
 }
 
 int attn_decode_max_splits(int max_seq) { return (max_seq + kAttnKeys - 1) / kAttnKeys; }
+
+hipError_t launch_decode_batch_parts(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
+                                     int max_seq, float *part, const SplitOut &out, int kvt, hipStream_t s) {
+  const int S = attn_decode_max_splits(max_seq);
+  dim3 grid(n_head, S, B);
+  if (kvt == kKvBf16) {
+    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvBf16>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part);
+  } else {
+    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvF32>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_combine_batch_kernel, dim3(n_head, B), dim3(64), 0, s, part, seqs, S, n_head * 64, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_batch(const BatchSeq *seqs, int B, const float *mel_emb, const float *mel_pos, int d, float *x,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(embed_batch_kernel, dim3(B), dim3(256), 0, s, seqs, mel_emb, mel_pos, d, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_advance_batch(const BatchSeq *seqs, int B, hipStream_t s) {
+  hipLaunchKernelGGL(advance_batch_kernel, dim3((B + 63) / 64), dim3(64), 0, s, seqs, B);
+  return hipGetLastError();
+}
 
 hipError_t launch_attn_decode(const float *q, const void *kc, const void *vc, int n_head,
                               int max_seq, const DecodeCtl *ctl, int static_len, float *part,

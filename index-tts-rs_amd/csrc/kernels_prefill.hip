@@ -413,8 +413,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
             } else {
               const int idx = n < 2 * d ? n - d : n - 2 * d;
               const int h = idx >> 6, e2 = idx & 63;
-              const size_t ci = ((size_t)h * a.qkv.max_seq + a.qkv.pos0 + m) * kHeadDim + e2;
               void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
+              int pos = a.qkv.pos0 + m;
+              if (a.qkv.seqs) {  // batched decode: row m is sequence m
+                const BatchSeq &sq = a.qkv.seqs[m];
+                if (sq.ctl->done) continue;
+                pos = sq.ctl->valid_len;
+                cache = static_cast<char *>(n < 2 * d ? sq.k : sq.v) +
+                        a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4);
+              }
+              const size_t ci = ((size_t)h * a.qkv.max_seq + pos) * kHeadDim + e2;
               if constexpr (KVT == kKvBf16) {
                 static_cast<uint16_t *>(cache)[ci] = (uint16_t)float_to_bf16_bits(v);
               } else {
@@ -511,18 +519,36 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
 }
 
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
+hipError_t set_cfg_attr() {
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes<BITS, PT, TM, TN>());
+}
+
+template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
 hipError_t launch_cfg(const GemmArgs &a, const Plan &p, hipStream_t s) {
   auto *fn = gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages>;
   constexpr size_t lds = lds_bytes<BITS, PT, TM, TN>();
-  static bool attr_set = false;  // per instantiation
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(256), lds, s, a, p.mode, p.nN, p.mt, p.S, p.gps);
   return hipGetLastError();
+}
+
+template <int BITS, int PT>
+hipError_t init_bits() {
+  hipError_t e = hipSuccess;
+  auto chk = [&](hipError_t x) {
+    if (e == hipSuccess) e = x;
+  };
+  chk(set_cfg_attr<BITS, PT, kEpiStore, 0, 1, 1>());
+  chk(set_cfg_attr<BITS, PT, kEpiStore, 0, 2, 2>());
+  chk(set_cfg_attr<BITS, PT, kEpiResid, 0, 1, 1>());
+  chk(set_cfg_attr<BITS, PT, kEpiResid, 0, 2, 2>());
+  chk(set_cfg_attr<BITS, PT, kEpiGelu, 0, 1, 1>());
+  chk(set_cfg_attr<BITS, PT, kEpiGelu, 0, 2, 2>());
+  chk(set_cfg_attr<BITS, PT, kEpiQKV, kKvBf16, 1, 1>());
+  chk(set_cfg_attr<BITS, PT, kEpiQKV, kKvBf16, 2, 2>());
+  chk(set_cfg_attr<BITS, PT, kEpiQKV, kKvF32, 1, 1>());
+  chk(set_cfg_attr<BITS, PT, kEpiQKV, kKvF32, 2, 2>());
+  return e;
 }
 
 template <int BITS, int PT, int EPI, int KVT>
@@ -549,6 +575,14 @@ hipError_t gemm_dispatch(const GemmArgs &a, const Plan &p, int epi, int kvt, hip
 }
 
 }  // namespace
+
+hipError_t gemm_init() {
+  hipError_t e = init_bits<8, kParamF16>();
+  if (e == hipSuccess) e = init_bits<8, kParamF32>();
+  if (e == hipSuccess) e = init_bits<4, kParamF16>();
+  if (e == hipSuccess) e = init_bits<4, kParamF32>();
+  return e;
+}
 
 size_t gemm_ws_floats(int n_cu) {
   // split-K is only chosen while tiles x splits stay within about two rounds of blocks

@@ -81,9 +81,16 @@ struct SamplerShared {
 __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n, const uint64_t *seen_in,
                                                            DevSampling p, uint64_t *rng_in,
                                                            int32_t *tok_out, DecodeCtl *ctl,
-                                                           int32_t *codes, int stop_tok, int mode) {
+                                                           int32_t *codes, int stop_tok, int mode,
+                                                           const DevSampling *ps, const BatchSeq *seqs) {
   __shared__ SamplerShared sh;
   extern __shared__ uint64_t sk[];  // [P] sort keys
+  if (seqs != nullptr) {  // batch: block b serves sequence b
+    ctl = seqs[blockIdx.x].ctl;
+    codes = seqs[blockIdx.x].codes;
+    p = ps[blockIdx.x];
+    logits += (size_t)blockIdx.x * n;
+  }
   if (mode == 1 && ctl->done) return;
   const uint64_t *seen = mode == 1 ? ctl->seen : seen_in;
   uint64_t *rng = mode == 1 ? &ctl->rng : rng_in;
@@ -352,7 +359,20 @@ hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSamplin
     lds = sizeof(uint64_t) * next_pow2((uint32_t)p.top_k);
   }
   hipLaunchKernelGGL(sampler_kernel, dim3(1), dim3(kThreads), lds, s, logits, n, seen, p, rng,
-                     tok_out, ctl, codes, stop_tok, mode);
+                     tok_out, ctl, codes, stop_tok, mode, nullptr, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_sampler_batch(float *logits, int n, const DevSampling *ps, const BatchSeq *seqs, int B,
+                                int stop_tok, int lds_top_k, bool any_sampled, hipStream_t s) {
+  if (n <= 0 || n > kThreads * kPerThread || B <= 0) return hipErrorInvalidValue;
+  size_t lds = 8;
+  if (any_sampled) {
+    if (lds_top_k < 1 || lds_top_k > n) return hipErrorInvalidValue;
+    lds = sizeof(uint64_t) * next_pow2((uint32_t)lds_top_k);
+  }
+  hipLaunchKernelGGL(sampler_kernel, dim3(B), dim3(kThreads), lds, s, logits, n, nullptr, DevSampling{}, nullptr,
+                     nullptr, nullptr, nullptr, stop_tok, 1, ps, seqs);
   return hipGetLastError();
 }
 

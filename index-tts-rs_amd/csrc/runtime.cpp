@@ -158,6 +158,10 @@ struct itts_gpt {
   DevBuf rk, rv, kstart, plog, pmap, pcodes, plp;
   int align_pairs[2][2] = {{4, 10}, {5, 10}};  // (layer, head), align/mod.rs:37
   int n_align = 2;
+  // batched decode: residual rows, q rows, split-form rows, attention partials, logits,
+  // the per-sequence descriptors and sampling parameters
+  DevBuf bx, bq, bpart, blog, bseqs, bps;
+  SplitBuf bh, ba, bf;
   // sampler API scratch
   DevBuf s_logits, s_seen, s_rng, s_tok;
   int ptype() const { return cfg.param_dtype == ITTS_F32 ? kParamF32 : kParamF16; }
@@ -613,6 +617,74 @@ itts_status check_replay_args(itts_gpt *g, itts_kv *kv, const int32_t *codes, in
   return ITTS_OK;
 }
 
+// Checks a batch of caches and uploads their descriptors; grows the batch workspace.
+itts_status prepare_batch(itts_gpt *g, itts_kv *const *caches, int B) {
+  const itts_config &c = g->cfg;
+  if (!caches || B <= 0 || B > 64) return set_error(ITTS_E_VALIDATION, "caches: 1..64 caches expected");
+  std::vector<BatchSeq> seqs(B);
+  for (int b = 0; b < B; b++) {
+    itts_kv *kv = caches[b];
+    if (!kv || kv->gpt != g) return set_error(ITTS_E_VALIDATION, "kv_cache: cache belongs to another decoder");
+    if (kv->max_seq != caches[0]->max_seq || kv->kvt != caches[0]->kvt)
+      return set_error(ITTS_E_VALIDATION, "kv_cache: a batch needs caches of one capacity and dtype");
+    for (int j = 0; j < b; j++)
+      if (caches[j] == kv) return set_error(ITTS_E_VALIDATION, "kv_cache: a cache appears twice in the batch");
+    seqs[b] = BatchSeq{kv->ctl.as<DecodeCtl>(), kv->k.p, kv->v.p, kv->codes.as<int32_t>()};
+  }
+  const int d = c.d_model, ms = caches[0]->max_seq;
+  HIP_TRY(g->bx.ensure(sizeof(float) * (size_t)B * d));
+  HIP_TRY(g->bq.ensure(sizeof(float) * (size_t)B * d));
+  HIP_TRY(g->bh.ensure(B, d));
+  HIP_TRY(g->ba.ensure(B, d));
+  HIP_TRY(g->bf.ensure(B, c.d_ffn));
+  HIP_TRY(g->bpart.ensure(sizeof(float) * (size_t)B * c.n_head * attn_decode_max_splits(ms) * 66));
+  HIP_TRY(g->blog.ensure(sizeof(float) * (size_t)B * c.mel_vocab));
+  HIP_TRY(g->bseqs.ensure(sizeof(BatchSeq) * B));
+  HIP_TRY(hipMemcpyAsync(g->bseqs.p, seqs.data(), sizeof(BatchSeq) * B, hipMemcpyHostToDevice, g->stream));
+  HIP_TRY(hipStreamSynchronize(g->stream));
+  return ITTS_OK;
+}
+
+// Enqueues one decode step of the B sequences described in gpt->bseqs (tokens, positions
+// and cache lengths read from their control blocks): logits land in gpt->blog [B][V] and
+// every unfinished sequence's cache length advances.  The linears run as M = B GEMMs, so
+// each weight byte is read once per step for the whole batch.
+itts_status enqueue_step_batch(itts_gpt *g, int B, int max_seq, int kvt) {
+  const itts_config &c = g->cfg;
+  const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
+  hipStream_t s = g->stream;
+  const BatchSeq *seqs = g->bseqs.as<BatchSeq>();
+  float *X = g->bx.as<float>();
+  HIP_TRY(launch_embed_batch(seqs, B, g->mel_emb.as<float>(), g->mel_pos.as<float>(), d, X, s));
+  const size_t layer_elems = (size_t)c.n_head * max_seq * 64;
+  for (int l = 0; l < c.n_layer; l++) {
+    const DevLayer &L = g->layers[l];
+    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, B, d, g->bh.out(), s));
+    GemmArgs ga = gemm_args(g, L.attn, g->bh.act(), B);
+    ga.qkv = QkvDst{g->bq.as<float>(), nullptr, nullptr, max_seq, 0, d, seqs, layer_elems * l};
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kvt, s));
+    HIP_TRY(launch_decode_batch_parts(g->bq.as<float>(), seqs, B, layer_elems * l, c.n_head, max_seq,
+                                      g->bpart.as<float>(), g->ba.out(), kvt, s));
+    ga = gemm_args(g, L.proj, g->ba.act(), B);
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kvt, s));
+    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, B, d, g->bh.out(), s));
+    ga = gemm_args(g, L.fc, g->bh.act(), B);
+    ga.xo = g->bf.out();
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kvt, s));
+    ga = gemm_args(g, L.mproj, g->bf.act(), B);
+    ga.y = X;
+    HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kvt, s));
+  }
+  HIP_TRY(launch_ln_rows(X, g->ln_f_w.as<float>(), g->ln_f_b.as<float>(), B, d, g->bh.out(), s, g->fn_w.as<float>(),
+                         g->fn_b.as<float>()));
+  GemmArgs ga = gemm_args(g, g->head, g->bh.act(), B);
+  ga.y = g->blog.as<float>();
+  HIP_TRY(launch_gemm(ga, bits, pt, kEpiStore, kvt, s));
+  HIP_TRY(launch_advance_batch(seqs, B, s));
+  return ITTS_OK;
+}
+
 // Writes the host-known fields of the decode control block (the device-owned step
 // counter that follows them is left alone).
 itts_status write_ctl(itts_kv *kv, const DecodeCtl &h) {
@@ -850,7 +922,7 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
     g->persist_ok = bits == 8 && coop != 0 && persist_init() == hipSuccess;
   }
   if (g->gws.ensure(sizeof(float) * gemm_ws_floats(g->n_cu)) || g->gcnt.ensure(sizeof(uint32_t) * kGemmCounters) ||
-      hipMemset(g->gcnt.p, 0, sizeof(uint32_t) * kGemmCounters))
+      hipMemset(g->gcnt.p, 0, sizeof(uint32_t) * kGemmCounters) || gemm_init() != hipSuccess)
     return fail(set_error(ITTS_E_DEVICE, "GEMM workspace allocation failed"));
   if (g->x.ensure(sizeof(float) * d) || g->q.ensure(sizeof(float) * d) || g->a.ensure(sizeof(float) * d) ||
       g->f.ensure(sizeof(float) * F) || g->logits.ensure(sizeof(float) * c.mel_vocab))
@@ -1311,6 +1383,165 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   *rng_state = fin.rng;
   kv->valid_len = fin.valid_len;
   return ITTS_OK;
+}
+
+itts_status itts_gpt_step_batch(itts_gpt *gpt, itts_kv *const *caches, int32_t batch, const int32_t *tokens,
+                                const int32_t *positions, float *logits_out) {
+  if (!gpt || !tokens || !positions) return set_error(ITTS_E_VALIDATION, "step_batch: null argument");
+  if (itts_status st = prepare_batch(gpt, caches, batch)) return st;
+  const itts_config &c = gpt->cfg;
+  for (int b = 0; b < batch; b++) {  // Gpt::step's checks, per sequence (gpt.rs:707-718)
+    itts_kv *kv = caches[b];
+    if (tokens[b] < 0 || tokens[b] >= c.mel_vocab)
+      return set_error(ITTS_E_VALIDATION, "mel_token_id: mel_token_id %d out of range 0..%d", tokens[b], c.mel_vocab);
+    if (positions[b] < 0 || positions[b] >= c.mel_pos_len)
+      return set_error(ITTS_E_VALIDATION, "pos_idx: pos_idx %d out of range 0..%d", positions[b], c.mel_pos_len);
+    if (kv->valid_len + 1 > kv->max_seq)
+      return set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
+                       kv->valid_len + 1, kv->max_seq);
+  }
+  for (int b = 0; b < batch; b++) {
+    DecodeCtl h{};
+    h.tok = tokens[b];
+    h.pos = positions[b];
+    h.valid_len = caches[b]->valid_len;
+    if (itts_status st = write_ctl(caches[b], h)) return st;
+  }
+  if (itts_status st = enqueue_step_batch(gpt, batch, caches[0]->max_seq, caches[0]->kvt)) return st;
+  if (logits_out)
+    HIP_TRY(hipMemcpyAsync(logits_out, gpt->blog.p, sizeof(float) * (size_t)batch * c.mel_vocab,
+                           hipMemcpyDeviceToHost, gpt->stream));
+  HIP_TRY(hipStreamSynchronize(gpt->stream));
+  for (int b = 0; b < batch; b++) caches[b]->valid_len += 1;
+  return ITTS_OK;
+}
+
+itts_status itts_generate_codes_batch(itts_gpt *gpt, itts_kv *const *caches, const itts_code_prompt *prompts,
+                                      const itts_sampling *params, int32_t batch, uint64_t *rng_states,
+                                      int32_t *codes_out, int32_t codes_cap, int32_t *n_codes) {
+  if (!gpt || !prompts || !params || !rng_states || !codes_out || !n_codes)
+    return set_error(ITTS_E_VALIDATION, "generate: null argument");
+  if (itts_status st = prepare_batch(gpt, caches, batch)) return st;
+  const itts_config &c = gpt->cfg;
+  std::vector<int> max_steps(batch), dev_steps(batch), T(batch);
+  std::vector<DevSampling> ds(batch);
+  int top_k_max = 1, longest = 0;
+  bool any_sampled = false;
+  for (int b = 0; b < batch; b++) {  // generate_codes_after's checks, per sequence
+    const itts_code_prompt &pr = prompts[b];
+    if (itts_status st = itts_sampling_validate(&params[b])) return st;
+    const int room = std::max(0, c.mel_pos_len - 3 - pr.n_prior);
+    max_steps[b] = std::min<int>((int)params[b].max_mel_tokens, room);
+    if (max_steps[b] == 0)
+      return set_error(ITTS_E_VALIDATION,
+                       "max_mel_tokens: no Mel positions left to generate (max_mel_tokens is 0 or the prior "
+                       "codes fill the capacity)");
+    if (codes_cap < max_steps[b])
+      return set_error(ITTS_E_VALIDATION, "codes_out: capacity %d < %d", codes_cap, max_steps[b]);
+    if (pr.min_codes < 0) return set_error(ITTS_E_VALIDATION, "min_codes: negative");
+    ds[b] = to_dev_sampling(params[b], c.mel_vocab);
+    if (!ds[b].greedy) {
+      any_sampled = true;
+      top_k_max = std::max(top_k_max, ds[b].top_k);
+    }
+  }
+  // prefill each prompt into its cache; its last-row logits seed the batch's first sample
+  for (int b = 0; b < batch; b++) {
+    itts_kv *kv = caches[b];
+    const itts_code_prompt &pr = prompts[b];
+    if (itts_status st = run_prefill(gpt, kv, pr.text_tokens, pr.n_text, pr.conds, pr.n_cond, pr.lang_id,
+                                     pr.prior_codes, pr.n_prior, &T[b]))
+      return st;
+    HIP_TRY(hipMemcpyAsync(gpt->blog.as<float>() + (size_t)b * c.mel_vocab, gpt->logits.p,
+                           sizeof(float) * c.mel_vocab, hipMemcpyDeviceToDevice, gpt->stream));
+    dev_steps[b] = std::min(max_steps[b], kv->max_seq - T[b] + 1);
+    longest = std::max(longest, dev_steps[b]);
+    DecodeCtl h{};
+    h.valid_len = T[b];
+    h.min_codes = pr.min_codes;
+    h.max_steps = dev_steps[b];
+    h.n_prior = pr.n_prior;
+    h.rng = rng_states[b];
+    h.last_tok = -1;
+    memset(h.seen, 0, sizeof h.seen);
+    h.seen[0] |= 1ull << 1;
+    const int start_mel = c.mel_vocab - 2;
+    h.seen[start_mel / 64] |= 1ull << (start_mel % 64);
+    *kv->host_ctl = h;
+    HIP_TRY(hipMemcpyAsync(kv->ctl.p, kv->host_ctl, offsetof(DecodeCtl, xstep), hipMemcpyHostToDevice,
+                           gpt->stream));
+    HIP_TRY(hipStreamSynchronize(gpt->stream));  // host_ctl is reused below
+  }
+  HIP_TRY(gpt->bps.ensure(sizeof(DevSampling) * batch));
+  HIP_TRY(hipMemcpyAsync(gpt->bps.p, ds.data(), sizeof(DevSampling) * batch, hipMemcpyHostToDevice, gpt->stream));
+  const int max_seq = caches[0]->max_seq, kvt = caches[0]->kvt;
+  auto enqueue_iteration = [&]() -> itts_status {
+    hipError_t le = launch_sampler_batch(gpt->blog.as<float>(), c.mel_vocab, gpt->bps.as<DevSampling>(),
+                                         gpt->bseqs.as<BatchSeq>(), batch, c.mel_vocab - 1, top_k_max, any_sampled,
+                                         gpt->stream);
+    if (le != hipSuccess) return set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
+    return enqueue_step_batch(gpt, batch, max_seq, kvt);
+  };
+  // one iteration (sample every sequence, then step the batch) captured once per call
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  auto release = [&]() {
+    if (gexec) (void)hipGraphExecDestroy(gexec);
+    if (graph) (void)hipGraphDestroy(graph);
+  };
+  if (gpt->use_graph) {
+    HIP_TRY(hipStreamSynchronize(gpt->stream));
+    HIP_TRY(hipStreamBeginCapture(gpt->stream, hipStreamCaptureModeThreadLocal));
+    itts_status es = enqueue_iteration();
+    hipError_t ce = hipStreamEndCapture(gpt->stream, &graph);
+    if (es) {
+      release();
+      return es;
+    }
+    if (ce == hipSuccess) ce = hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0);
+    if (ce != hipSuccess) {
+      release();
+      return set_error(ITTS_E_DEVICE, "graph capture failed: %s", hipGetErrorName(ce));
+    }
+  }
+  // replay in chunks of 8 iterations; finished sequences skip their work, so the batch
+  // runs until every sequence is done (at most the longest sequence's steps)
+  std::vector<DecodeCtl> fin(batch);
+  const int chunk = 8;
+  hipError_t e = hipSuccess;
+  for (int it = 0; it < longest && e == hipSuccess;) {
+    for (int i = 0; i < chunk && it < longest; i++, it++) {
+      if (gexec) {
+        e = hipGraphLaunch(gexec, gpt->stream);
+      } else if (enqueue_iteration() != ITTS_OK) {
+        e = hipErrorLaunchFailure;
+      }
+      if (e != hipSuccess) break;
+    }
+    for (int b = 0; b < batch && e == hipSuccess; b++)
+      e = hipMemcpyAsync(&fin[b], caches[b]->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost, gpt->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(gpt->stream);
+    bool all = true;
+    for (int b = 0; b < batch; b++) all = all && fin[b].done;
+    if (all) break;
+  }
+  release();
+  HIP_TRY(e);
+  for (int b = 0; b < batch; b++)
+    if (!fin[b].done) return set_error(ITTS_E_INTERNAL, "generation did not reach its end");
+  itts_status result = ITTS_OK;
+  for (int b = 0; b < batch; b++) {
+    itts_kv *kv = caches[b];
+    kv->valid_len = fin[b].valid_len;
+    n_codes[b] = fin[b].n_codes;
+    rng_states[b] = fin[b].rng;
+    HIP_TRY(hipMemcpy(codes_out + (size_t)b * codes_cap, kv->codes.p, sizeof(int32_t) * fin[b].n_codes,
+                      hipMemcpyDeviceToHost));
+    if (dev_steps[b] < max_steps[b] && fin[b].n_codes == dev_steps[b] && result == ITTS_OK)
+      result = set_error(ITTS_E_CAPACITY, "kv_cache: sequence length %d exceeds KV cache capacity %d",
+                         kv->max_seq + 1, kv->max_seq);
+  }
+  return result;
 }
 
 itts_status itts_kv_last_timing(const itts_kv *kv, itts_timing *out) {

@@ -140,6 +140,9 @@ _SIGS = {
                                                C.c_int32, C.c_void_p]),
     "itts_gpt_set_alignment_heads": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32]),
     "itts_gpt_forward_logits": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+    "itts_gpt_step_batch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "itts_generate_codes_batch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
+                                            C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
     "itts_gpt_prefill_after": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                          C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
                                          C.c_int32, C.c_void_p]),
@@ -485,6 +488,42 @@ def generate_codes_after(gpt: Gpt, prompt: CodePrompt, cache: KvCache, params: S
     _check(lib.itts_generate_codes_after(gpt._h, cache._h, C.byref(cp), C.byref(sp),
                                          C.byref(rng.state), _ptr(out), cap, C.byref(n)))
     return out[: n.value].copy()
+
+
+def step_batch(gpt: Gpt, caches, tokens, positions, logits=True):
+    """One batched decode step: Gpt::step for every (cache, token, position); returns
+    logits [batch][mel_vocab]."""
+    arr = (C.c_void_p * len(caches))(*[c._h for c in caches])
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    p = np.ascontiguousarray(positions, dtype=np.int32)
+    out = np.empty((len(caches), gpt.cfg["mel_vocab"]), np.float32) if logits else None
+    _check(lib.itts_gpt_step_batch(gpt._h, C.cast(arr, C.c_void_p), len(caches), _ptr(t), _ptr(p), _ptr(out)))
+    return out
+
+
+def generate_codes_batch(gpt: Gpt, prompts, caches, params, rngs):
+    """generate_codes_after for several sequences stepped together; params and rngs are
+    per sequence (the rngs advance as SamplerRng does).  Returns a list of code arrays."""
+    B = len(prompts)
+    keep, arr = [], (itts_code_prompt * B)()
+    for i, pr in enumerate(prompts):
+        t = np.ascontiguousarray(pr.text_tokens, dtype=np.int32)
+        c = np.ascontiguousarray(pr.conds, dtype=np.float32).reshape(-1, gpt.cfg["d_model"])
+        pp = np.ascontiguousarray(pr.prior_codes if pr.prior_codes is not None else [], dtype=np.int32)
+        keep += [t, c, pp]
+        arr[i] = itts_code_prompt(_ptr(t), len(t), _ptr(c), c.shape[0], int(pr.lang_id), _ptr(pp), len(pp),
+                                  int(pr.min_codes))
+    sp = (itts_sampling * B)(*[p.to_c() for p in params])
+    cs = (C.c_void_p * B)(*[c._h for c in caches])
+    states = np.array([r.state.value for r in rngs], dtype=np.uint64)
+    cap = max(1, max(int(p.max_mel_tokens) for p in params))
+    out = np.empty((B, cap), np.int32)
+    n = np.empty(B, np.int32)
+    _check(lib.itts_generate_codes_batch(gpt._h, C.cast(cs, C.c_void_p), C.cast(arr, C.c_void_p),
+                                         C.cast(sp, C.c_void_p), B, _ptr(states), _ptr(out), cap, _ptr(n)))
+    for r, st in zip(rngs, states):
+        r.state.value = int(st)
+    return [out[i, : n[i]].copy() for i in range(B)]
 
 
 def generate_codes(gpt: Gpt, text_tokens, conds, lang_id, cache, params, rng) -> np.ndarray:

@@ -183,3 +183,24 @@ def test_full_forward_logits_batch(full):
     err = float(np.abs(got - ref).max())
     say(f"[gpu]   rows {got.shape[0]}, max |logit diff| {err:.3g}")
     assert got.shape == ref.shape and err < 1e-4
+
+
+def test_full_generate_batch(full):
+    """Four sequences decoded together at the real shape (fp32 caches): per sequence, the
+    greedy ids (penalty 10) equal the oracle's for that sequence alone."""
+    W, g, M = full
+    say("[gpu] full generate_codes_batch, 4 sequences")
+    prompts, refs = [], []
+    lengths = [24, 32, 16, 28]
+    for b in range(4):
+        pr = synth.make_prompt(W.cfg, 32, 40 + 20 * b, seed=60 + b)
+        p = H.SamplingParams(greedy=True, repetition_penalty=10.0, max_mel_tokens=lengths[b])
+        prompts.append((H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, lengths[b]), p))
+        ref, _, _ = M.generate_codes_after(M.kv(2048, kv_bf16=False), pr.text_tokens, pr.conds, pr.lang_id, p, 0,
+                                           min_codes=lengths[b])
+        refs.append(ref.tolist())
+    caches = [g.kv_cache(2048, H.ITTS_F32) for _ in range(4)]
+    got = H.generate_codes_batch(g, [c for c, _ in prompts], caches, [p for _, p in prompts],
+                                 [H.SamplerRng(0) for _ in range(4)])
+    for b in range(4):
+        assert got[b].tolist() == refs[b], b
