@@ -14,7 +14,8 @@ achieved = algorithmic bytes of one decode step / its average device time (HIP e
 on the decoder's stream).
 
 The default run also reports, under "secondary", the prefill-heavy workload (4 x 547
-rows, all-row logits, MFMA-bound) and the int4 decode workload.
+rows, all-row logits, MFMA-bound), the batch-8 decode workload and the int4 decode
+workload.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload long|short|int4]
 """
@@ -141,6 +142,39 @@ def prefill_heavy(H, synth, g, cfg, seed):
             "note": "fp16 MFMA with hi/lo split activations (two products per weight)"}
 
 
+def batch_decode(H, synth, g, cfg, seed):
+    """The batched workload: 8 sentences with text lengths U[20, 200] and decode lengths
+    U[200, 1200] (seeded), each stopping at its own length (STOP masked until then),
+    sampled (T 0.8, top-k 30, top-p 0.8, penalty 10), bf16 caches of 2048 rows.  One
+    generate_codes_batch call: 8 prefills, then one batched step per token while any
+    sequence runs.  Aggregate rate = all generated tokens / host call time."""
+    rng = np.random.default_rng(seed + 100)
+    n_text = rng.integers(20, 201, 8)
+    n_dec = rng.integers(200, 1201, 8)
+    prompts, params = [], []
+    for b in range(8):
+        pr = synth.make_prompt(cfg, 32, int(n_text[b]), seed=seed + 200 + b)
+        prompts.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, int(n_dec[b])))
+        params.append(H.SamplingParams(greedy=False, temperature=0.8, top_k=30, top_p=0.8,
+                                       repetition_penalty=10.0, max_mel_tokens=int(n_dec[b])))
+    caches = [g.kv_cache(2048, H.ITTS_BF16) for _ in range(8)]
+    H.generate_codes_batch(g, prompts, caches, params, [H.SamplerRng(b) for b in range(8)])
+    t0 = time.perf_counter()
+    codes = H.generate_codes_batch(g, prompts, caches, params, [H.SamplerRng(b) for b in range(8)])
+    wall = time.perf_counter() - t0
+    total = sum(len(c) for c in codes)
+    assert [len(c) for c in codes] == [int(x) for x in n_dec]
+    steps = int(n_dec.max())
+    print(f"[bench] batch-8 decode: {total / wall:.1f} tokens/s aggregate", file=sys.stderr, flush=True)
+    return {"workload": "batch 8 sentences, text lengths U[20,200], decode lengths U[200,1200] with per-sequence "
+                        "stop, sampled (T 0.8, top-k 30, top-p 0.8, penalty 10), bf16 caches of 2048 rows",
+            "text_lengths": [int(x) for x in n_text], "decode_lengths": [int(x) for x in n_dec],
+            "tokens": total, "ms": round(wall * 1e3, 2),
+            "aggregate_tokens_per_s": round(total / wall, 1),
+            "per_sequence_tokens_per_s": round(steps / wall, 1),
+            "note": "host call time includes the 8 prefills; one batched step per token of the longest sequence"}
+
+
 def int4_decode(H, synth, seed):
     """The int4 workload: 4-bit weights, prefill 32 + 128 text (163 rows), 1500 greedy
     steps with STOP masked; device-timed decode rate and the HBM roofline of one step."""
@@ -178,7 +212,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill-heavy (4 x 547 rows) and int4 decode measurements")
-    ap.add_argument("--only", choices=["prefill", "prefill-heavy"],
+    ap.add_argument("--only", choices=["prefill", "prefill-heavy", "batch8"],
                     help="for profilers: only repeat the workload's prefill or the prefill-heavy "
                          "forward --repeat times, print one line per call, no JSON")
     ap.add_argument("--repeat", type=int, default=6)
@@ -210,6 +244,10 @@ def main():
         for b in range(4):
             pr = synth.make_prompt(cfg, 32, 512, seed=args.seed + 10 + b)
             heavy.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None))
+        if args.only == "batch8":
+            r = batch_decode(H, synth, g, cfg, args.seed)
+            print(f"[bench] batch8: {r['aggregate_tokens_per_s']} tokens/s aggregate", flush=True)
+            return
         for i in range(args.repeat):
             t0 = time.perf_counter()
             if args.only == "prefill":
@@ -312,7 +350,8 @@ def main():
                      "bytes_per_launch": bytes_step, "mean_keys": mean_L},
     }
     if not args.no_secondary and args.workload == "long":
-        out["secondary"] = {"prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed)}
+        out["secondary"] = {"prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed),
+                            "batch8_decode": batch_decode(H, synth, g, cfg, args.seed)}
         del g, kv
         out["secondary"]["int4_decode"] = int4_decode(H, synth, args.seed)
     if not args.no_cpu_baseline:
