@@ -181,7 +181,7 @@ struct PersistArgs {
   int xin_len, part_len, own_len, out_len, pp_len, lp_len;
 };
 // Whether the persistent step supports this shape on B blocks; *S = attention splits.
-bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int *S);
+bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int bits, int *S);
 constexpr size_t kPersistMaxLds = 150 * 1024;
 size_t persist_lds_bytes(const PersistArgs &a);
 // 16-byte words of the exchange arrays x_x, x_qkv, x_part, x_attn, x_mid, x_f: total, and
@@ -189,8 +189,8 @@ size_t persist_lds_bytes(const PersistArgs &a);
 size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]);
 // Whether one block of the persistent kernel with `lds` bytes of dynamic LDS fits a
 // compute unit (threads, static + dynamic LDS).
-hipError_t persist_fits(int ptype, size_t lds, bool *fits);
-hipError_t launch_decode_persist(PersistArgs a, int ptype, hipStream_t s);
+hipError_t persist_fits(int bits, int ptype, size_t lds, bool *fits);
+hipError_t launch_decode_persist(PersistArgs a, int bits, int ptype, hipStream_t s);
 // Raises the kernel's dynamic-LDS limit; once per process, outside stream capture.
 hipError_t persist_init();
 

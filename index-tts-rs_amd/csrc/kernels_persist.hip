@@ -27,7 +27,7 @@
 //   loaders  (waves 7-15) : loads only, all unconditional - the weight slices (ahead of
 //                           use) and the attention K/V rows (LDS-DMA); they compute the
 //                           dot products and row sums in LDS.
-// Each role is its own instantiation of the step program (run<PT, ROLE>), all executing
+// Each role is its own instantiation of the step program (run<BITS, PT, ROLE>), all executing
 // the same sequence of __syncthreads, which on gfx950 waits for LDS traffic only.
 //
 // Ownership.  For a matrix with N rows, block b owns rows [N*b/B, N*(b+1)/B).  A block's
@@ -67,7 +67,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct RowMap {
-  int row0, rows, C;  // first row, row count, 16-byte chunks per row
+  int row0, rows, C;  // first row, row count, 16-byte chunks per row (K/16 int8, K/32 int4)
 };
 
 __device__ inline int row_start(int N, int b, int B) { return (int)((long)N * b / B); }
@@ -238,16 +238,18 @@ struct Slots {
   typename ParamReg<PT>::type p[NS];
 };
 
-// Loader lane ll (0..575) loads its chunks of the block's rows of ql (int8 codes).  The
-// rows are contiguous and a row is C = K/16 chunks, so chunk c of the block sits at
-// codes + row0*K + 16c with its group parameters at params[row0*K/64 + c/4].  Every load
-// is issued (a chunk past the block's share reads chunk 0 instead, row row0 < N always
-// exists), so the number of loads in flight is the same on every path.
-template <int PT, int NS>
+// Loader lane ll (0..575) loads its chunks of the block's rows of ql.  The rows are
+// contiguous and a row is C 16-byte chunks (16 int8 or 32 int4 codes), so chunk c of the
+// block sits at codes + row0*K*BITS/8 + 16c with its group parameters at
+// params[row0*K/64 + c/(64/codes per chunk)].  Every load is issued (a chunk past the
+// block's share reads chunk 0 instead, row row0 < N always exists), so the number of loads
+// in flight is the same on every path.
+template <int BITS, int PT, int NS>
 __device__ inline void load_slots(Slots<PT, NS> &s, const DevQL &ql, const RowMap &m, int ll) {
   using P = typename ParamReg<PT>::type;
+  constexpr uint32_t kGroupShift = BITS == 8 ? 2 : 1;  // chunks per group: 4 or 2
   const int total = m.rows * m.C;
-  const char *cb = reinterpret_cast<const char *>(ql.codes + (size_t)m.row0 * ql.K);
+  const char *cb = reinterpret_cast<const char *>(ql.codes + (size_t)m.row0 * ql.K * BITS / 8);
   const char *pb = reinterpret_cast<const char *>(static_cast<const P *>(ql.params) + (size_t)m.row0 * (ql.K / kGroup));
   uint32_t lo = (uint32_t)ll;
   asm volatile("" : "+v"(lo));
@@ -256,8 +258,29 @@ __device__ inline void load_slots(Slots<PT, NS> &s, const DevQL &ql, const RowMa
     uint32_t c = lo + (uint32_t)(kLoadThreads * j);
     c = (int)c < total ? c : 0u;
     s.c[j] = gld<u32x4>(cb + c * 16u);
-    s.p[j] = gld<P>(pb + (c >> 2) * (uint32_t)sizeof(P));
+    s.p[j] = gld<P>(pb + (c >> kGroupShift) * (uint32_t)sizeof(P));
   }
+}
+
+// 32 4-bit codes (low nibble first) against 32 activations: (sum of code*x, sum of x).
+__device__ inline float2 dot32(const u32x4 c, const float *xc) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  float acc = 0.0f, xs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float4 xa = *reinterpret_cast<const float4 *>(xc + 8 * i);
+    const float4 xb = *reinterpret_cast<const float4 *>(xc + 8 * i + 4);
+    acc += xa.x * (float)(w[i] & 0xfu);
+    acc += xa.y * (float)((w[i] >> 4) & 0xfu);
+    acc += xa.z * (float)((w[i] >> 8) & 0xfu);
+    acc += xa.w * (float)((w[i] >> 12) & 0xfu);
+    acc += xb.x * (float)((w[i] >> 16) & 0xfu);
+    acc += xb.y * (float)((w[i] >> 20) & 0xfu);
+    acc += xb.z * (float)((w[i] >> 24) & 0xfu);
+    acc += xb.w * (float)(w[i] >> 28);
+    xs += ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+  }
+  return make_float2(acc, xs);
 }
 
 // 16 codes against 16 activations: (sum of code*x, sum of x).
@@ -278,7 +301,7 @@ __device__ inline float2 dot16(const u32x4 c, const float *xc) {
 
 // Loaders: per-chunk partial products into part[] (LDS): scale * sum(code*x) + bias *
 // sum(x), the group affine folded per 16-value chunk.
-template <int PT, int NS>
+template <int BITS, int PT, int NS>
 __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const float *xn, float *part, int ll) {
   const int total = m.rows * m.C;
   // per-slot chunk indices are recomputed per call rather than hoisted out of the layer
@@ -291,7 +314,7 @@ __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const 
     if (c < total) {
       const int kc = c % m.C;
       const float2 p = param_value(s.p[j]);
-      const float2 r = dot16(s.c[j], xn + kc * 16);
+      const float2 r = BITS == 8 ? dot16(s.c[j], xn + kc * 16) : dot32(s.c[j], xn + kc * 32);
       part[c] = p.x * r.x + p.y * r.y;
     }
     // one chunk's activations in registers at a time
@@ -438,7 +461,7 @@ enum Role : int { kRolePoll = 0, kRolePub = 1, kRoleLoad = 2 };
 // sequence of __syncthreads; each contains only its role's work, so the compiler allocates
 // registers per role (a role branch on a divergent condition would be linearised and make
 // every wave hold the registers of all roles).
-template <int PT, int ROLE>
+template <int BITS, int PT, int ROLE>
 __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, float *lds) {
   constexpr bool poller = ROLE == kRolePoll, pub = ROLE == kRolePub, loader = ROLE == kRoleLoad;
   DecodeCtl *ctl = a.ctl;
@@ -475,11 +498,12 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   int *rs_3d = rs_d + (B + 1);
   int *rs_f = rs_3d + (B + 1);
 
-  const RowMap m_qkv = rows_of(3 * d, d / 16, b, B);
-  const RowMap m_proj = rows_of(d, d / 16, b, B);
-  const RowMap m_fc = rows_of(F, d / 16, b, B);
-  const RowMap m_mp = rows_of(d, F / 16, b, B);
-  const RowMap m_head = rows_of(a.V, d / 16, b, B);
+  constexpr int EPC = BITS == 8 ? 16 : 32;  // codes per 16-byte chunk
+  const RowMap m_qkv = rows_of(3 * d, d / EPC, b, B);
+  const RowMap m_proj = rows_of(d, d / EPC, b, B);
+  const RowMap m_fc = rows_of(F, d / EPC, b, B);
+  const RowMap m_mp = rows_of(d, F / EPC, b, B);
+  const RowMap m_head = rows_of(a.V, d / EPC, b, B);
   // bias rows inside a layer's parameter buffer
   const int bo_q = 4 * d, bo_p = bo_q + m_qkv.rows, bo_f = bo_p + m_proj.rows, bo_m = bo_f + m_fc.rows;
   const bool attn_block = b < H * S;
@@ -492,8 +516,8 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   Slots<PT, kSlFc> wf;
   Slots<PT, kSlMp> wm;
   if (loader) {
-    load_slots<PT>(wq, a.layers[0].attn, m_qkv, ll);
-    load_slots<PT>(wp, a.layers[0].proj, m_proj, ll);
+    load_slots<BITS, PT>(wq, a.layers[0].attn, m_qkv, ll);
+    load_slots<BITS, PT>(wp, a.layers[0].proj, m_proj, ll);
   }
   if (poller) {
     for (int i = tid; i < d; i += kPollThreads)
@@ -529,7 +553,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       if (sh.abort) return;
     }
     layer_norm(xin, xn, lp, lp + d, d, sh.red, T);
-    if (loader) dot_slots(wq, m_qkv, xn, part, ll);
+    if (loader) dot_slots<BITS>(wq, m_qkv, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_qkv, part, lp + bo_q, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
@@ -550,7 +574,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // stores, well before the next layer reads them
     if (pub) stage_params_dma(a, l + 1, lpb + ((l + 1) & 1) * a.lp_len, m_qkv, m_proj, m_fc, m_mp, m_head, lane);
     // fc weights: needed after the attention, c_proj and an exchange (the longest lead)
-    if (loader) load_slots<PT>(wf, Ly.fc, m_fc, ll);
+    if (loader) load_slots<BITS, PT>(wf, Ly.fc, m_fc, ll);
     // ---------------- P2: attention split of head ah over keys [j0, j1) ----------------
     if (attn_block) {
       // cached K/V rows of the split (the appended row comes from the exchange), copied
@@ -775,7 +799,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    if (loader) dot_slots(wp, m_proj, xin, part, ll);
+    if (loader) dot_slots<BITS>(wp, m_proj, xin, part, ll);
     __syncthreads();
     if (loader)
       row_sums(m_proj, part, lp + bo_p, lw, lane, [&](int r, float v) {
@@ -787,13 +811,13 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (pub) publish_rows(a.x_mid, d, B, b, out, m_proj.rows, ep + 4u, lane);
     // prefetches are issued once the phase's outputs are out (issuing them earlier delays
     // the row sums behind the memory pipeline)
-    if (loader) load_slots<PT>(wm, Ly.mproj, m_mp, ll);
+    if (loader) load_slots<BITS, PT>(wm, Ly.mproj, m_mp, ll);
     // ---------------- P4: LN2, c_fc rows + GELU ------------------------------------
     if (poller && !poll_rows(a.x_mid, d, B, rs_d, ep + 4u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
     layer_norm(xin, xn, lp + 2 * d, lp + 3 * d, d, sh.red, T);
-    if (loader) dot_slots(wf, m_fc, xn, part, ll);
+    if (loader) dot_slots<BITS>(wf, m_fc, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_fc, part, lp + bo_f, lw, lane, [&](int r, float v) { out[r] = gelu_tanh(v); });
     __syncthreads();
@@ -801,12 +825,12 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       publish_rows(a.x_f, F, B, b, out, m_fc.rows, ep + 5u, lane);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // next layer's parameter copies
     }
-    if (loader && l + 1 < a.n_layer) load_slots<PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
+    if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
     // ---------------- P5: mlp c_proj rows + residual ---------------------------------
     if (poller && !poll_rows(a.x_f, F, B, rs_f, ep + 5u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    if (loader) dot_slots(wm, m_mp, xin, part, ll);
+    if (loader) dot_slots<BITS>(wm, m_mp, xin, part, ll);
     __syncthreads();
     if (loader)
       row_sums(m_mp, part, lp + bo_m, lw, lane, [&](int r, float v) {
@@ -816,12 +840,12 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       });
     __syncthreads();
     if (pub) publish_rows(a.x_x, d, B, b, out, m_mp.rows, ep + 6u, lane);
-    if (loader && l + 1 < a.n_layer) load_slots<PT>(wp, a.layers[l + 1].proj, m_proj, ll);
+    if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wp, a.layers[l + 1].proj, m_proj, ll);
   }
   // ---------------- head: ln_f, final_norm, mel_head rows -> logits ------------------
   {
     Slots<PT, kSlHead> wh;
-    if (loader) load_slots<PT>(wh, a.head, m_head, ll);
+    if (loader) load_slots<BITS, PT>(wh, a.head, m_head, ll);
     const uint32_t ep = ep0 + (uint32_t)(a.n_layer - 1) * 8u;
     const float *lp = lpb + (a.n_layer & 1) * a.lp_len;
     if (poller && !poll_rows(a.x_x, d, B, rs_d, ep + 6u, xin, err, tid)) sh.abort = 1;
@@ -829,7 +853,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (sh.abort) return;
     layer_norm(xin, xn, lp, lp + d, d, sh.red, tid);
     layer_norm(xn, xn, lp + 2 * d, lp + 3 * d, d, sh.red, tid);
-    if (loader) dot_slots(wh, m_head, xn, part, ll);
+    if (loader) dot_slots<BITS>(wh, m_head, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_head, part, lp + 4 * d, lw, lane, [&](int r, float v) { out[r] = v; });
     __syncthreads();
@@ -846,7 +870,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   }
 }
 
-template <int PT>
+template <int BITS, int PT>
 __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a) {
   __shared__ PersistShared sh;
   extern __shared__ float lds[];
@@ -857,17 +881,26 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
   }
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (wave >= kLoadWave0)
-    run<PT, kRoleLoad>(a, sh, lds);
+    run<BITS, PT, kRoleLoad>(a, sh, lds);
   else if (wave == kPubWave)
-    run<PT, kRolePub>(a, sh, lds);
+    run<BITS, PT, kRolePub>(a, sh, lds);
   else
-    run<PT, kRolePoll>(a, sh, lds);
+    run<BITS, PT, kRolePoll>(a, sh, lds);
+}
+
+const void *persist_fn(int bits, int ptype) {
+  if (bits == 4)
+    return ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<4, kParamF16>)
+                              : reinterpret_cast<const void *>(decode_persist_kernel<4, kParamF32>);
+  return ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<8, kParamF16>)
+                            : reinterpret_cast<const void *>(decode_persist_kernel<8, kParamF32>);
 }
 
 }  // namespace
 
-bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int *S_out) {
-  if (B < 1 || H < 1 || d % 64 != 0 || F % 64 != 0 || n_layer < 1) return false;
+bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int bits, int *S_out) {
+  if (B < 1 || H < 1 || d % 64 != 0 || F % 64 != 0 || n_layer < 1 || (bits != 8 && bits != 4)) return false;
+  const int epc = bits == 8 ? 16 : 32;
   const int S = std::min(12, B / H);
   if (S < 1) return false;
   if ((max_seq + S - 1) / S > kKeySlots * kKeyPasses) return false;
@@ -876,8 +909,8 @@ bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int
   auto fits = [&](int N, int C, int slots) {
     return (long)((N + B - 1) / B) * C <= (long)slots * kLoadThreads;
   };
-  if (!fits(3 * d, d / 16, kSlQkv) || !fits(d, d / 16, kSlProj) || !fits(F, d / 16, kSlFc) ||
-      !fits(d, F / 16, kSlMp) || !fits(V, d / 16, kSlHead))
+  if (!fits(3 * d, d / epc, kSlQkv) || !fits(d, d / epc, kSlProj) || !fits(F, d / epc, kSlFc) ||
+      !fits(d, F / epc, kSlMp) || !fits(V, d / epc, kSlHead))
     return false;
   *S_out = S;
   return true;
@@ -900,26 +933,24 @@ size_t persist_lds_bytes(const PersistArgs &a) {
   return f * sizeof(float);
 }
 
-hipError_t launch_decode_persist(PersistArgs a, int ptype, hipStream_t s) {
+hipError_t launch_decode_persist(PersistArgs a, int bits, int ptype, hipStream_t s) {
   void *args[] = {&a};
   const size_t lds = persist_lds_bytes(a);
-  const void *fn = ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<kParamF16>)
-                                      : reinterpret_cast<const void *>(decode_persist_kernel<kParamF32>);
-  return hipLaunchCooperativeKernel(fn, dim3(a.B), dim3(kThreads), args, (unsigned)lds, s);
+  return hipLaunchCooperativeKernel(persist_fn(bits, ptype), dim3(a.B), dim3(kThreads), args, (unsigned)lds, s);
 }
 
 hipError_t persist_init() {
-  for (const void *fn : {reinterpret_cast<const void *>(decode_persist_kernel<kParamF16>),
-                         reinterpret_cast<const void *>(decode_persist_kernel<kParamF32>)}) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPersistMaxLds);
-    if (e != hipSuccess) return e;
-  }
+  for (int bits : {8, 4})
+    for (int pt : {kParamF16, kParamF32}) {
+      hipError_t e = hipFuncSetAttribute(persist_fn(bits, pt), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)kPersistMaxLds);
+      if (e != hipSuccess) return e;
+    }
   return hipSuccess;
 }
 
-hipError_t persist_fits(int ptype, size_t lds, bool *fits) {
-  const void *fn = ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<kParamF16>)
-                                      : reinterpret_cast<const void *>(decode_persist_kernel<kParamF32>);
+hipError_t persist_fits(int bits, int ptype, size_t lds, bool *fits) {
+  const void *fn = persist_fn(bits, ptype);
   hipFuncAttributes fa{};
   hipError_t e = hipFuncGetAttributes(&fa, fn);
   if (e != hipSuccess) return e;

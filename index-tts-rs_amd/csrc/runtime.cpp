@@ -144,7 +144,7 @@ struct itts_gpt {
   // persistent decode step: device copy of `layers`, blocks (one per compute unit)
   DevBuf dlayers;
   int n_cu = 0;
-  bool persist_ok = false;  // kernels set up and 8-bit codes
+  bool persist_ok = false;  // kernels set up (int8 or int4 codes)
   itts_decode_path path = ITTS_DECODE_AUTO;
   // decode workspace
   DevBuf x, q, a, f, logits;
@@ -399,7 +399,7 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
 // the device): logits land in gpt->logits and ctl->valid_len advances.
 itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
   if (kv->persist) {
-    HIP_TRY(launch_decode_persist(kv->pa, g->ptype(), g->stream));
+    HIP_TRY(launch_decode_persist(kv->pa, g->cfg.quant_bits, g->ptype(), g->stream));
     return ITTS_OK;
   }
   const itts_config &c = g->cfg;
@@ -718,7 +718,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
   int S = 0;
   const bool shape_ok = g->persist_ok && kv->kvt == kKvBf16 &&
                         persist_supported(c.d_model, c.d_ffn, c.mel_vocab, c.n_head, c.n_layer, kv->max_seq,
-                                          g->n_cu, &S);
+                                          g->n_cu, c.quant_bits, &S);
   PersistArgs a{};
   const int d = c.d_model, F = c.d_ffn, H = c.n_head, V = c.mel_vocab, B = g->n_cu;
   if (shape_ok) {
@@ -733,14 +733,15 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     auto rows = [&](int N) { return (N + B - 1) / B; };
     const int rq = rows(3 * d), rp = rows(d), rf = rows(F), rh = rows(V);
     a.xin_len = std::max(d, F);
-    a.part_len = r4(std::max({rq * (d / 16), rp * (d / 16), rf * (d / 16), rp * (F / 16), rh * (d / 16)}));
+    const int epc = c.quant_bits == 8 ? 16 : 32;  // codes per 16-byte chunk
+    a.part_len = r4(std::max({rq * (d / epc), rp * (d / epc), rf * (d / epc), rp * (F / epc), rh * (d / epc)}));
     a.own_len = r4(rp);
     a.out_len = r4(std::max({rq, rp, rf, rh}));
     a.pp_len = r4(S * 66);
     a.lp_len = r4(4 * d + std::max(rq + rp + rf + rp, rh));
   }
   bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
-  if (ok) HIP_TRY(persist_fits(g->ptype(), persist_lds_bytes(a), &ok));  // one block per CU
+  if (ok) HIP_TRY(persist_fits(c.quant_bits, g->ptype(), persist_lds_bytes(a), &ok));  // one block per CU
   if (g->path == ITTS_DECODE_PERSISTENT && !ok)
     return set_error(ITTS_E_VALIDATION,
                      "decode_path: the persistent decode step does not support this cache (bf16 rows, "
@@ -919,7 +920,7 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
         hipDeviceGetAttribute(&g->n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
-    g->persist_ok = bits == 8 && coop != 0 && persist_init() == hipSuccess;
+    g->persist_ok = (bits == 8 || bits == 4) && coop != 0 && persist_init() == hipSuccess;
   }
   if (g->gws.ensure(sizeof(float) * gemm_ws_floats(g->n_cu)) || g->gcnt.ensure(sizeof(uint32_t) * kGemmCounters) ||
       hipMemset(g->gcnt.p, 0, sizeof(uint32_t) * kGemmCounters) || gemm_init() != hipSuccess)

@@ -204,3 +204,27 @@ def test_full_generate_batch(full):
                                  [H.SamplerRng(0) for _ in range(4)])
     for b in range(4):
         assert got[b].tolist() == refs[b], b
+
+
+@pytest.mark.parametrize("path", [H.ITTS_DECODE_AUTO, H.ITTS_DECODE_MULTI])
+def test_full_int4_steps(path):
+    """4-bit weights at the real shape (persistent step by default, or the multi-kernel
+    step): prefill of 32 + 128 text ids and 16 teacher-forced steps against the oracle."""
+    say(f"[gpu] full int4 decoder, path {path}")
+    W = synth.make_weights(dict(synth.FULL_CONFIG, quant_bits=4), seed=13)
+    g = H.Gpt(W)
+    M = ito.Model(W)
+    try:
+        g.set_decode_path(path)
+        pr = synth.make_prompt(W.cfg, 32, 128, seed=3)
+        kv = g.kv_cache(2048)
+        assert kv.decode_path() == (H.ITTS_DECODE_PERSISTENT if path == H.ITTS_DECODE_AUTO else H.ITTS_DECODE_MULTI)
+        okv = M.kv(2048)
+        worst = float(np.abs(g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv) -
+                             M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)).max())
+        for i, t in enumerate(np.random.default_rng(4).integers(0, 8192, 16)):
+            worst = max(worst, float(np.abs(g.step(kv, int(t), i + 2) - M.step(okv, int(t), i + 2)).max()))
+        say(f"[gpu]   worst max |logit diff| {worst:.3g}")
+        assert worst < LOGIT_TOL and worst < 2e-3
+    finally:
+        g.close()
