@@ -418,33 +418,52 @@ __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, fl
   rows(mm, Ly->mproj.bias);
 }
 
-// Block-wide sum over the 1024 threads (same order on every block); red is this
-// reduction's own scratch, so one barrier suffices.
-__device__ inline float bsum(float v, float *red, int tid) {
-  v = wave64_sum(v);
-  if ((tid & 63) == 0) red[tid >> 6] = v;
-  __syncthreads();
-  float t = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kThreads / 64; i++) t += red[i];
-  return t;
-}
-
 // LayerNorm (biased variance, eps 1e-5) of the LDS row x into the LDS row y (y may be x),
-// w and b in LDS.  red holds 32 floats (two reductions' scratch).
+// w and b in LDS (16-byte aligned, n a multiple of 4, n <= 4 * 1024); red holds 32 floats.
+// Thread t < n/4 holds values 4t..4t+3 of x, w and b, read with one 16-byte LDS load each,
+// all three issued together, so the row is read once and every later pass works from
+// registers.  The waves holding values form the sums; every wave adds the wave sums in the
+// same order.
 __device__ __forceinline__ void layer_norm(const float *x, float *y, const float *w, const float *b, int n, float *red,
                                            int tid) {
-  float s = 0.0f;
-  for (int i = tid; i < n; i += kThreads) s += x[i];
-  const float mean = bsum(s, red, tid) / (float)n;
-  float q = 0.0f;
-  for (int i = tid; i < n; i += kThreads) {
-    const float dv = x[i] - mean;
-    q += dv * dv;
+  const int nq = n >> 2, nwv = (nq + 63) >> 6;
+  const bool act = tid < nq, wact = tid < nwv * 64;
+  float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), wv = xv, bv = xv;
+  if (act) {
+    xv = reinterpret_cast<const float4 *>(x)[tid];
+    wv = reinterpret_cast<const float4 *>(w)[tid];
+    bv = reinterpret_cast<const float4 *>(b)[tid];
   }
-  const float var = bsum(q, red + 16, tid) / (float)n;
-  const float rstd = 1.0f / sqrtf(var + 1e-5f);
-  for (int i = tid; i < n; i += kThreads) y[i] = (x[i] - mean) * rstd * w[i] + b[i];
+  if (wact) {
+    const float s = wave64_sum((xv.x + xv.y) + (xv.z + xv.w));
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+  }
+  __syncthreads();
+  float mean = 0.0f;
+  if (wact) {
+    float t = 0.0f;
+    for (int i = 0; i < nwv; i++) t += red[i];
+    mean = t / (float)n;
+    float q = 0.0f;
+    if (act) {
+      const float d0 = xv.x - mean, d1 = xv.y - mean, d2 = xv.z - mean, d3 = xv.w - mean;
+      q = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    q = wave64_sum(q);
+    if ((tid & 63) == 0) red[16 + (tid >> 6)] = q;
+  }
+  __syncthreads();
+  if (act) {
+    float t = 0.0f;
+    for (int i = 0; i < nwv; i++) t += red[16 + i];
+    const float rstd = 1.0f / sqrtf(t / (float)n + 1e-5f);
+    float4 yv;
+    yv.x = (xv.x - mean) * rstd * wv.x + bv.x;
+    yv.y = (xv.y - mean) * rstd * wv.y + bv.y;
+    yv.z = (xv.z - mean) * rstd * wv.z + bv.z;
+    yv.w = (xv.w - mean) * rstd * wv.w + bv.w;
+    reinterpret_cast<float4 *>(y)[tid] = yv;
+  }
   __syncthreads();
 }
 
@@ -899,7 +918,8 @@ const void *persist_fn(int bits, int ptype) {
 }  // namespace
 
 bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int bits, int *S_out) {
-  if (B < 1 || H < 1 || d % 64 != 0 || F % 64 != 0 || n_layer < 1 || (bits != 8 && bits != 4)) return false;
+  if (B < 1 || H < 1 || d % 64 != 0 || d > 4 * kThreads || F % 64 != 0 || n_layer < 1 || (bits != 8 && bits != 4))
+    return false;
   const int epc = bits == 8 ? 16 : 32;
   const int S = std::min(12, B / H);
   if (S < 1) return false;
