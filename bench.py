@@ -14,8 +14,8 @@ achieved = algorithmic bytes of one decode step / its average device time (HIP e
 on the decoder's stream).
 
 The default run also reports, under "secondary", the prefill-heavy workload (4 x 547
-rows, all-row logits, MFMA-bound), the batch-8 decode workload and the int4 decode
-workload.
+rows, all-row logits, MFMA-bound), the batch-8 decode workload, the int4 decode
+workload and the Stage-2 CFM estimator's 25-step solve for 10 s of audio.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload long|short|int4]
 """
@@ -202,6 +202,56 @@ def int4_decode(H, synth, seed):
             "hbm_achieved_gbs": round(achieved, 1), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)}
 
 
+def cfm_flops(c: dict, B: int, T: int) -> float:
+    """Algorithmic FLOPs of one forward_merged over B x T rows (2 per multiply-add): the
+    linears, WaveNet's convolutions and the attention products."""
+    d, F, C_, L, NL, K = c["dim"], c["inter"], c["in_ch"], c["n_layers"], c["wn_layers"], c["wn_kernel"]
+    R = B * T
+    md = 2 * C_ + d + c["style_dim"]
+    f = 2.0 * R * md * d
+    f += L * 2.0 * R * d * (3 * d + d + 2 * F) + L * 2.0 * R * F * d + L * 4.0 * B * T * T * d
+    f += (L - 1 - L // 2) * 2.0 * R * 2 * d * d
+    f += 2.0 * R * (d + C_) * d + 2.0 * R * d * d
+    f += sum(2.0 * R * K * d * 2 * d + 2.0 * R * d * (d if i + 1 == NL else 2 * d) for i in range(NL))
+    f += 2.0 * R * d * d * 2 + 2.0 * R * d * C_
+    return f
+
+
+def cfm_solve(seed):
+    """The Stage-2 CFM estimator (cfm.rs, reference shape: dim 512, 13 layers, 8 heads,
+    SwiGLU 1536, WaveNet 8 x kernel 5) in its 25-step Euler solve with CFG 0.7 for 10 s of
+    audio: 861 generated frames (22,050 Hz / hop 256 = 86.13 frames/s) after a 172-frame
+    prompt (the reference fixture's ref_mel), T_total 1033, the CFG pair as batch 2.  The
+    reference's figure for the same stage and audio length is 1,540 ms (M-series GPU,
+    docs/benchmarks/indextts-rust-verification-and-benchmark-report.md:135)."""
+    from itts_hip import synth
+    from itts_hip.cfm import FULL_CONFIG, CfmDit
+    W = synth.make_cfm_weights(FULL_CONFIG, seed=seed)
+    m = CfmDit(W, FULL_CONFIG)
+    inp = synth.make_cfm_inputs(FULL_CONFIG, 1033, 172, seed=seed)
+    args = (inp["cat_condition"], inp["ref_mel"], inp["style"], inp["noise_z"], 25, 0.7)
+    m.solve_euler(*args)
+    walls, devs = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        m.solve_euler(*args)
+        walls.append((time.perf_counter() - t0) * 1e3)
+        devs.append(m.last_timing_ms())
+    m.close()
+    dev = statistics.median(devs)
+    tflop = 25 * cfm_flops(FULL_CONFIG, 2, 1033) / 1e12
+    print(f"[bench] CFM 25-step solve (10 s of audio): {dev:.1f} ms device, {statistics.median(walls):.1f} ms host",
+          file=sys.stderr, flush=True)
+    return {"workload": "CFM DiT 25-step Euler solve, CFG 0.7, T_total 1033 (172 prompt + 861 generated frames = "
+                        "10 s of audio), batch 2 (CFG pair), fp32, seeded weights of the reference shape",
+            "solve_ms": round(dev, 2), "host_call_ms": round(statistics.median(walls), 2),
+            "reference_ms": 1540.0, "speedup_vs_reference": round(1540.0 / dev, 2),
+            "tflop_per_solve": round(tflop, 3), "achieved_tflops": round(tflop / (dev * 1e-3), 1),
+            "peak_tflops": 157.3, "frac": round(tflop / (dev * 1e-3) / 157.3, 4),
+            "note": "fp32: linears and WaveNet convolutions in rocBLAS sgemm, attention and elementwise in HIP "
+                    "kernels; peak = fp32 MFMA dense"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -212,7 +262,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill-heavy (4 x 547 rows) and int4 decode measurements")
-    ap.add_argument("--only", choices=["prefill", "prefill-heavy", "batch8"],
+    ap.add_argument("--only", choices=["prefill", "prefill-heavy", "batch8", "cfm"],
                     help="for profilers: only repeat the workload's prefill or the prefill-heavy "
                          "forward --repeat times, print one line per call, no JSON")
     ap.add_argument("--repeat", type=int, default=6)
@@ -244,6 +294,10 @@ def main():
         for b in range(4):
             pr = synth.make_prompt(cfg, 32, 512, seed=args.seed + 10 + b)
             heavy.append(H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None))
+        if args.only == "cfm":
+            r = cfm_solve(args.seed)
+            print(f"[bench] cfm: {r['solve_ms']} ms per 25-step solve", flush=True)
+            return
         if args.only == "batch8":
             r = batch_decode(H, synth, g, cfg, args.seed)
             print(f"[bench] batch8: {r['aggregate_tokens_per_s']} tokens/s aggregate", flush=True)
@@ -354,6 +408,7 @@ def main():
                             "batch8_decode": batch_decode(H, synth, g, cfg, args.seed)}
         del g, kv
         out["secondary"]["int4_decode"] = int4_decode(H, synth, args.seed)
+        out["secondary"]["cfm_solve"] = cfm_solve(args.seed)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(W, prompt, sp, args.cpu_steps)

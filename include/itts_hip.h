@@ -299,6 +299,38 @@ itts_status itts_qlinear_forward(itts_gpt *gpt, const itts_qlinear *ql, int32_t 
 itts_status itts_decode_timing(itts_gpt *gpt, itts_kv *kv, int32_t mel_token_id, int32_t pos_idx,
                                int32_t n_steps, float *ms_per_step);
 
+/* ---- Stage-2 CFM DiT estimator and Euler / CFG solver (crates/core/src/models/cfm.rs) ----
+ * Replaces CfmDit (cfm.rs:411-761): the 13-layer U-ViT transformer (AdaLN over RMSNorm,
+ * rope, SwiGLU, long skips), skip_linear / conv1, the 8-layer WaveNet, the final layer
+ * and conv2, evaluated in fp32 on the device, and the 25-step Euler integration with
+ * classifier-free guidance.  Weights are fp32, by checkpoint tensor name. */
+typedef struct itts_cfm itts_cfm;
+typedef struct itts_cfm_config {
+  /* reference values (cfm.rs:36-61): 512, 13, 8, 1536, 80, 192, 8, 5; dim == 64 * n_heads */
+  int32_t dim, n_layers, n_heads, inter, in_ch, style_dim, wn_layers, wn_kernel;
+} itts_cfm_config;
+/* CfmDit::from_weights (cfm.rs:460-531): n tensors, names[i] the checkpoint name (e.g.
+ * "transformer.layers.3.attention.wqkv.weight"), data[i] its fp32 values (host) and
+ * numel[i] its element count, checked against the shape the name requires.  Errors:
+ * ITTS_E_WEIGHT naming a missing tensor or one of the wrong size; ITTS_E_VALIDATION for an
+ * unsupported configuration. */
+itts_status itts_cfm_create(const itts_cfm_config *cfg, const char *const *names, const float *const *data,
+                            const int64_t *numel, int32_t n, itts_cfm **out);
+void itts_cfm_destroy(itts_cfm *cfm);
+/* forward_merged (cfm.rs:545-617): x_t [B][T][in_ch], x_merged [B][T][2*in_ch+dim+style],
+ * t [B] (host) -> out [B][in_ch][T] (host). */
+itts_status itts_cfm_forward(itts_cfm *cfm, const float *x_t, const float *x_merged, const float *t, int32_t B,
+                             int32_t T, float *out);
+/* solve_euler (cfm.rs:619-760): cat_condition [T_total][dim], ref_mel [in_ch][T_ref],
+ * style [style_dim], noise_z [in_ch][T_total] (host) -> mel_out [in_ch][T_total - T_ref]
+ * (host).  Errors as the reference: n_timesteps >= 1, T_ref < T_total. */
+itts_status itts_cfm_solve_euler(itts_cfm *cfm, const float *cat_condition, int32_t T_total, const float *ref_mel,
+                                 int32_t T_ref, const float *style, const float *noise_z, int32_t n_timesteps,
+                                 float cfg_rate, float *mel_out);
+/* Device time of the last itts_cfm_solve_euler's integration loop (HIP events), in ms.
+ * No counterpart in the reference: a measurement helper. */
+itts_status itts_cfm_last_solve_ms(itts_cfm *cfm, float *ms);
+
 #ifdef __cplusplus
 }
 #endif

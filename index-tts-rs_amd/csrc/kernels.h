@@ -209,4 +209,26 @@ hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSamplin
 hipError_t launch_sampler_batch(float *logits, int n, const DevSampling *ps, const BatchSeq *seqs, int B,
                                 int stop_tok, int lds_top_k, bool any_sampled, hipStream_t s);
 
+// ---- Stage-2 CFM DiT estimator (kernels_cfm.hip); activations [B][T][C] fp32 ----
+hipError_t cfm_temb(const float *t, int B, float *emb /*[B][256]*/, hipStream_t s);
+hipError_t cfm_silu(const float *x, float *y, int n, hipStream_t s);
+hipError_t cfm_bias_rows(float *C, int ldc, const float *bias, int rows, int cols, hipStream_t s);
+hipError_t cfm_add_bias(float *C, int ldc, const float *bias, int rows, int cols, hipStream_t s);
+hipError_t cfm_adaln(const float *x, float *y, int R, int T, int d, const float *mod, int ld_mod, const float *norm_w,
+                     hipStream_t s);
+hipError_t cfm_final_norm(const float *x, float *y, int R, int T, int d, const float *mod, hipStream_t s);
+hipError_t cfm_attention(const float *qkv, int B, int T, int d, int H, float *out, hipStream_t s);
+hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);
+hipError_t cfm_gate(const float *acts, const float *in_b, const float *g, int ld_g, int R, int T, int d, float *act,
+                    hipStream_t s);
+hipError_t cfm_res_skip(const float *rs, const float *rs_b, int last, int R, int T, int d, int pad, float *h,
+                        float *out, hipStream_t s);
+hipError_t cfm_euler_prep(float *x, int C, int T, int T_ref, float *xt, float *merged, int MD, hipStream_t s);
+hipError_t cfm_euler_update(float *x, const float *v, int C, int T, float dt, float cfg, hipStream_t s);
+hipError_t cfm_static_tail(float *merged, int MD, int C, int d, int S, int T, const float *ref_mel, int T_ref,
+                           const float *style, hipStream_t s);
+hipError_t cfm_transpose_tc(const float *v, int B, int T, int C, float *out, hipStream_t s);
+hipError_t cfm_pad_rows(const float *x, int B, int T, int d, int pad, float *hp, hipStream_t s);
+hipError_t cfm_fill(float *p, int n, float v, hipStream_t s);
+
 }  // namespace itts

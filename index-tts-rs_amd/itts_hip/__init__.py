@@ -108,6 +108,12 @@ class itts_timing(C.Structure):
                 ("decode_steps", C.c_int32), ("samples", C.c_int32)]
 
 
+class itts_cfm_config(C.Structure):
+    """CFM DiT estimator shape (cfm.rs:36-61); the head dimension is 64."""
+    _fields_ = [(n, C.c_int32) for n in ("dim", "n_layers", "n_heads", "inter", "in_ch", "style_dim",
+                                         "wn_layers", "wn_kernel")]
+
+
 _SIGS = {
     "itts_kv_last_timing": (C.c_int, [C.c_void_p, C.POINTER(itts_timing)]),
     "itts_version": (C.c_char_p, []),
@@ -170,6 +176,14 @@ _SIGS = {
                                        C.c_int32, C.c_int, C.c_void_p, C.c_int32, C.c_void_p]),
     "itts_decode_timing": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                      C.POINTER(C.c_float)]),
+    "itts_cfm_create": (C.c_int, [C.POINTER(itts_cfm_config), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
+                                  C.POINTER(C.c_void_p)]),
+    "itts_cfm_destroy": (None, [C.c_void_p]),
+    "itts_cfm_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                   C.c_void_p]),
+    "itts_cfm_solve_euler": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p,
+                                       C.c_void_p, C.c_int32, C.c_float, C.c_void_p]),
+    "itts_cfm_last_solve_ms": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGS)

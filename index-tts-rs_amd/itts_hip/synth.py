@@ -218,3 +218,41 @@ def save_safetensors(W: ModelWeights, path: str, drop: tuple = (), override: dic
     t = {k: np.ascontiguousarray(v) for k, v in t.items()}
     save_file(t, path, metadata={"format": "mlx"})
     return t
+
+
+# ---- Stage-2 CFM DiT estimator ----------------------------------------------------------
+def make_cfm_weights(cfg: dict, seed: int = 0) -> dict:
+    """Seeded random-init CFM estimator tensors by checkpoint name (cfm.rs:460-531), float32.
+
+    Linear and convolution weights are N(0, 1/fan_in) so activations stay O(1) through the
+    13-layer stack; biases N(0, 0.02); RMSNorm weights 1 + N(0, 0.1); AdaLN projection biases
+    1 + N(0, 0.1) for the scale half and N(0, 0.1) for the shift half, so that every
+    modulation path is exercised.  Each tensor draws from its own stream keyed by
+    (seed, tensor index)."""
+    from .cfm import tensor_shapes
+    out = {}
+    for i, (name, shape) in enumerate(tensor_shapes(cfg).items()):
+        g = np.random.Generator(np.random.PCG64([seed, 7919, i]))
+        if name.endswith("norm.weight"):
+            a = 1.0 + 0.1 * g.standard_normal(shape)
+        elif name.endswith("project_layer.bias") or name.endswith("adaLN_modulation.layers.1.bias"):
+            half = shape[0] // 2
+            a = 0.1 * g.standard_normal(shape)
+            if name.endswith("project_layer.bias"):
+                a[:half] += 1.0
+        elif name.endswith(".bias"):
+            a = 0.02 * g.standard_normal(shape)
+        else:
+            fan_in = int(np.prod(shape[1:]))
+            a = g.standard_normal(shape) / np.sqrt(fan_in)
+        out[name] = np.ascontiguousarray(a, dtype=np.float32)
+    return out
+
+
+def make_cfm_inputs(cfg: dict, t_total: int, t_ref: int, seed: int = 0) -> dict:
+    """Seeded solve_euler inputs of the reference's shapes (cfm.rs:621-632): cat_condition
+    [1, T_total, dim], ref_mel [1, in_ch, T_ref], style [1, style], noise_z [1, in_ch, T_total]."""
+    g = np.random.Generator(np.random.PCG64([seed, 104729]))
+    f = lambda *s: g.standard_normal(s).astype(np.float32)
+    return dict(cat_condition=f(1, t_total, cfg["dim"]), ref_mel=f(1, cfg["in_ch"], t_ref),
+                style=f(1, cfg["style_dim"]), noise_z=f(1, cfg["in_ch"], t_total))

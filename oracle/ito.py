@@ -307,3 +307,118 @@ def seen_init(start_mel=8192):
     w = np.zeros(129, np.uint64)
     lib.ito_seen_init(_p(w), start_mel)
     return w
+
+
+# ---- Stage-2 CFM DiT estimator (cfm.rs) ---------------------------------------------------
+class ito_cfm_config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("dim", "n_layers", "n_heads", "inter", "in_ch", "style_dim",
+                                         "wn_layers", "wn_kernel")]
+
+
+class ito_cfm_adaln(C.Structure):
+    _fields_ = [("proj_w", C.c_void_p), ("proj_b", C.c_void_p), ("norm_w", C.c_void_p)]
+
+
+class ito_cfm_temb(C.Structure):
+    _fields_ = [("w0", C.c_void_p), ("b0", C.c_void_p), ("w2", C.c_void_p), ("b2", C.c_void_p)]
+
+
+class ito_cfm_block(C.Structure):
+    _fields_ = [("attn_norm", ito_cfm_adaln), ("ffn_norm", ito_cfm_adaln), ("wqkv", C.c_void_p),
+                ("wo", C.c_void_p), ("w1", C.c_void_p), ("w3", C.c_void_p), ("w2", C.c_void_p),
+                ("skip_w", C.c_void_p), ("skip_b", C.c_void_p)]
+
+
+class ito_cfm_wn_layer(C.Structure):
+    _fields_ = [("in_w", C.c_void_p), ("in_b", C.c_void_p), ("rs_w", C.c_void_p), ("rs_b", C.c_void_p)]
+
+
+class ito_cfm(C.Structure):
+    _fields_ = [("cfg", ito_cfm_config), ("cond_proj_w", C.c_void_p), ("cond_proj_b", C.c_void_p),
+                ("merge_w", C.c_void_p), ("merge_b", C.c_void_p), ("t1", ito_cfm_temb), ("t2", ito_cfm_temb),
+                ("blocks", C.POINTER(ito_cfm_block)), ("tnorm", ito_cfm_adaln),
+                ("skip_w", C.c_void_p), ("skip_b", C.c_void_p), ("conv1_w", C.c_void_p), ("conv1_b", C.c_void_p),
+                ("res_w", C.c_void_p), ("res_b", C.c_void_p), ("wn_cond_w", C.c_void_p), ("wn_cond_b", C.c_void_p),
+                ("wn", C.POINTER(ito_cfm_wn_layer)), ("fada_w", C.c_void_p), ("fada_b", C.c_void_p),
+                ("flin_w", C.c_void_p), ("flin_b", C.c_void_p), ("conv2_w", C.c_void_p), ("conv2_b", C.c_void_p)]
+
+
+_CFM_SIGS = {
+    "ito_cfm_rope": (None, [C.c_void_p, C.c_int32, C.c_int32]),
+    "ito_cfm_timestep": (None, [C.POINTER(ito_cfm_temb), C.c_int32, C.c_float, C.c_void_p]),
+    "ito_cfm_forward": (C.c_int, [C.POINTER(ito_cfm), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                  C.c_void_p]),
+    "ito_cfm_solve_euler": (C.c_int, [C.POINTER(ito_cfm), C.c_void_p, C.c_int32, C.c_void_p, C.c_int32,
+                                      C.c_void_p, C.c_void_p, C.c_int32, C.c_float, C.c_void_p]),
+}
+for _n, (_r, _a) in _CFM_SIGS.items():
+    getattr(lib, _n).restype = _r
+    getattr(lib, _n).argtypes = _a
+
+
+class CfmModel:
+    """The oracle's CFM estimator over a dict of float32 tensors keyed by checkpoint name."""
+
+    def __init__(self, weights: dict, cfg: dict):
+        self.cfg = dict(cfg)
+        self._keep = {k: np.ascontiguousarray(v, np.float32) for k, v in weights.items()}
+        w = lambda n: self._keep[n].ctypes.data
+        adaln = lambda p: ito_cfm_adaln(w(f"{p}.project_layer.weight"), w(f"{p}.project_layer.bias"),
+                                        w(f"{p}.norm.weight"))
+        temb = lambda p: ito_cfm_temb(w(f"{p}.mlp.layers.0.weight"), w(f"{p}.mlp.layers.0.bias"),
+                                      w(f"{p}.mlp.layers.2.weight"), w(f"{p}.mlp.layers.2.bias"))
+        L = cfg["n_layers"]
+        self._blocks = (ito_cfm_block * L)()
+        for i in range(L):
+            p = f"transformer.layers.{i}"
+            self._blocks[i] = ito_cfm_block(adaln(f"{p}.attention_norm"), adaln(f"{p}.ffn_norm"),
+                                            w(f"{p}.attention.wqkv.weight"), w(f"{p}.attention.wo.weight"),
+                                            w(f"{p}.feed_forward.w1.weight"), w(f"{p}.feed_forward.w3.weight"),
+                                            w(f"{p}.feed_forward.w2.weight"), w(f"{p}.skip_in_linear.weight"),
+                                            w(f"{p}.skip_in_linear.bias"))
+        NL = cfg["wn_layers"]
+        self._wn = (ito_cfm_wn_layer * NL)()
+        for i in range(NL):
+            self._wn[i] = ito_cfm_wn_layer(w(f"wavenet.in_layers.{i}.weight"), w(f"wavenet.in_layers.{i}.bias"),
+                                           w(f"wavenet.res_skip_layers.{i}.weight"),
+                                           w(f"wavenet.res_skip_layers.{i}.bias"))
+        self.m = ito_cfm(ito_cfm_config(**cfg), w("cond_projection.weight"), w("cond_projection.bias"),
+                         w("cond_x_merge_linear.weight"), w("cond_x_merge_linear.bias"), temb("t_embedder"),
+                         temb("t_embedder2"), self._blocks, adaln("transformer.norm"), w("skip_linear.weight"),
+                         w("skip_linear.bias"), w("conv1.weight"), w("conv1.bias"), w("res_projection.weight"),
+                         w("res_projection.bias"), w("wavenet.cond_layer.weight"), w("wavenet.cond_layer.bias"),
+                         self._wn, w("final_layer.adaLN_modulation.layers.1.weight"),
+                         w("final_layer.adaLN_modulation.layers.1.bias"), w("final_layer.linear.weight"),
+                         w("final_layer.linear.bias"), w("conv2.weight"), w("conv2.bias"))
+
+    def timestep(self, which: int, t: float) -> np.ndarray:
+        out = np.empty(self.cfg["dim"], np.float32)
+        lib.ito_cfm_timestep(C.byref(self.m.t1 if which == 1 else self.m.t2), self.cfg["dim"], t, _p(out))
+        return out
+
+    def forward_merged(self, x_t, x_merged, t) -> np.ndarray:
+        x_t = np.ascontiguousarray(x_t, np.float32)
+        x_merged = np.ascontiguousarray(x_merged, np.float32)
+        t = np.ascontiguousarray(t, np.float32)
+        B, T = x_t.shape[:2]
+        out = np.empty((B, self.cfg["in_ch"], T), np.float32)
+        check(lib.ito_cfm_forward(C.byref(self.m), _p(x_t), _p(x_merged), _p(t), B, T, _p(out)))
+        return out
+
+    def solve_euler(self, cat_condition, ref_mel, style, noise_z, n_timesteps=25, cfg_rate=0.7) -> np.ndarray:
+        cc = np.ascontiguousarray(cat_condition, np.float32)
+        rm = np.ascontiguousarray(ref_mel, np.float32)
+        st = np.ascontiguousarray(style, np.float32)
+        nz = np.ascontiguousarray(noise_z, np.float32)
+        T, Tr = cc.shape[1], rm.shape[2]
+        out = np.empty((1, self.cfg["in_ch"], max(T - Tr, 0)), np.float32)
+        check(lib.ito_cfm_solve_euler(C.byref(self.m), _p(cc), T, _p(rm), Tr, _p(st), _p(nz), n_timesteps,
+                                      cfg_rate, _p(out)))
+        return out
+
+
+def cfm_rope(x: np.ndarray, n_heads: int) -> np.ndarray:
+    """The oracle's rope (traditional pairs) on a copy of x [T, n_heads*64]."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib.ito_cfm_rope(_p(y), y.shape[0], n_heads)
+    return y

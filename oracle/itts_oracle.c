@@ -667,3 +667,8 @@ int ito_generate_codes_after(const ito_model *m, ito_kv *kv, int32_t mode, const
   *n_codes = n;
   return rc;
 }
+
+/* ------------------------------------------------------------------ */
+/* Stage-2 CFM DiT estimator and Euler solver                          */
+/* ------------------------------------------------------------------ */
+#include "cfm_oracle.inc"

@@ -1,5 +1,6 @@
 /*
- * itts_oracle — CPU restatement of the index-tts-rs Stage-1 GPT decoder.
+ * itts_oracle — CPU restatement of the index-tts-rs Stage-1 GPT decoder and of the
+ * Stage-2 CFM DiT estimator with its Euler solver.
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP decoder is
  * compared against.  Only tests/, __graft_entry__.smoke() and the cpu_baseline leg
@@ -157,6 +158,69 @@ int ito_generate_codes_after(const ito_model *m, ito_kv *kv, int32_t mode, const
                              int32_t min_codes, const ito_sampling *p, uint64_t *rng_state,
                              int32_t *codes_out, int32_t codes_cap, int32_t *n_codes,
                              float *first_logits /* optional [mel_vocab] */);
+
+/* ---- CFM DiT estimator and Euler / classifier-free-guidance solver (cfm.rs) ----
+ * Restates crates/core/src/models/cfm.rs: compute_rope_freqs 73-101, TimestepEmbedder
+ * 104-147, AdaLn 150-183, TransformerBlock::forward 253-313, WaveNet::forward 373-408,
+ * CfmDit::forward_merged 545-617, CfmDit::solve_euler 619-760.  The MLX primitives those
+ * call (rms_norm, rope with traditional=true, scaled_dot_product_attention without a mask,
+ * conv1d, layer_norm without affine parameters, silu / tanh / sigmoid) are restated from
+ * their published definitions.  Activations are [B][T][C] row-major; dot products
+ * accumulate in double, elementwise functions are fp32 libm calls.  The head dimension is
+ * 64 and the timestep frequency embedding 256 wide, as in the reference; everything else
+ * comes from the configuration (the reference's values: dim 512, 13 layers, 8 heads,
+ * inter 1536, in_ch 80, style 192, 8 WaveNet layers of kernel 5). */
+typedef struct {
+  int32_t dim, n_layers, n_heads, inter, in_ch, style_dim, wn_layers, wn_kernel;
+} ito_cfm_config;
+typedef struct {
+  const float *proj_w, *proj_b, *norm_w; /* [2*dim][dim], [2*dim], [dim] */
+} ito_cfm_adaln;
+typedef struct {
+  const float *w0, *b0, *w2, *b2; /* [dim][256], [dim], [dim][dim], [dim] */
+} ito_cfm_temb;
+typedef struct {
+  ito_cfm_adaln attn_norm, ffn_norm;
+  const float *wqkv;           /* [3*dim][dim] (no bias) */
+  const float *wo;             /* [dim][dim] */
+  const float *w1, *w3;        /* [inter][dim] */
+  const float *w2;             /* [dim][inter] */
+  const float *skip_w, *skip_b; /* [dim][2*dim], [dim]: used by layers > n_layers/2 */
+} ito_cfm_block;
+typedef struct {
+  const float *in_w, *in_b; /* [2*dim][wn_kernel][dim], [2*dim] */
+  const float *rs_w, *rs_b; /* [rs][dim], [rs]; rs = dim for the last layer, else 2*dim */
+} ito_cfm_wn_layer;
+typedef struct {
+  ito_cfm_config cfg;
+  const float *cond_proj_w, *cond_proj_b; /* [dim][dim], [dim] */
+  const float *merge_w, *merge_b;         /* [dim][2*in_ch + dim + style], [dim] */
+  ito_cfm_temb t1, t2;
+  const ito_cfm_block *blocks;            /* [n_layers] */
+  ito_cfm_adaln tnorm;
+  const float *skip_w, *skip_b;           /* [dim][dim + in_ch], [dim] */
+  const float *conv1_w, *conv1_b;         /* [dim][dim], [dim] */
+  const float *res_w, *res_b;             /* [dim][dim], [dim] */
+  const float *wn_cond_w, *wn_cond_b;     /* [2*dim*wn_layers][dim], [2*dim*wn_layers] */
+  const ito_cfm_wn_layer *wn;             /* [wn_layers] */
+  const float *fada_w, *fada_b;           /* [2*dim][dim], [2*dim] */
+  const float *flin_w, *flin_b;           /* [dim][dim], [dim] */
+  const float *conv2_w, *conv2_b;         /* [in_ch][dim], [in_ch] */
+} ito_cfm;
+/* rope(traditional=true, base 10000, offset 0) of n_heads 64-wide heads, in place on
+ * x [T][n_heads*64]: pair (2i, 2i+1) of a head at position t turns by t * 10000^(-2i/64). */
+void ito_cfm_rope(float *x, int32_t T, int32_t n_heads);
+/* TimestepEmbedder::forward for one t: out [dim]. */
+void ito_cfm_timestep(const ito_cfm_temb *e, int32_t dim, float t, float *out);
+/* forward_merged: x_t [B][T][in_ch], x_merged [B][T][2*in_ch + dim + style], t [B] ->
+ * out [B][in_ch][T]. */
+int ito_cfm_forward(const ito_cfm *m, const float *x_t, const float *x_merged, const float *t, int32_t B,
+                    int32_t T, float *out);
+/* solve_euler: cat_condition [T_total][dim], ref_mel [in_ch][T_ref], style [style],
+ * noise [in_ch][T_total] -> out [in_ch][T_total - T_ref]. */
+int ito_cfm_solve_euler(const ito_cfm *m, const float *cat_condition, int32_t T_total, const float *ref_mel,
+                        int32_t T_ref, const float *style, const float *noise, int32_t n_timesteps,
+                        float cfg_rate, float *out);
 
 const char *ito_last_error(void);
 void ito_set_threads(int32_t n);
