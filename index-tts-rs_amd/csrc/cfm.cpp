@@ -106,7 +106,8 @@ struct itts_cfm {
   std::vector<WnLayer> wn;
   // per-forward workspace (sized for R = B*T rows)
   Buf emb, th, t1, t2, st, mods, wng, fmod, tdev;
-  Buf hA, hB, n, qkv, att, gu, act, xres, hpad, acts, rs, oacc, v;
+  Buf hA, hB, n, qkv, att, gu, act, xres, hpad, acts, rs, oacc, v, rope;
+  int rope_T = 0;  // sequence length the rope table holds
   std::vector<Buf> skips;
   // solve / API staging
   Buf x, xt, merged, catc, refm, sty, io_a, io_b;
@@ -157,6 +158,11 @@ itts_status ensure_rows(itts_cfm *m, int B, int T) {
   CK(m->oacc.ensure(R * d));
   CK(m->v.ensure(R * c.in_ch));
   for (auto &b : m->skips) CK(b.ensure(R * d));
+  if (m->rope_T != T) {
+    CK(m->rope.ensure((size_t)T * 64));
+    CK(cfm_rope_table(T, m->rope.p, m->s));
+    m->rope_T = T;
+  }
   return ITTS_OK;
 }
 
@@ -214,7 +220,7 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     const float *mod_a = m->mods.p + (size_t)(2 * i) * 2 * d, *mod_f = m->mods.p + (size_t)(2 * i + 1) * 2 * d;
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_a, na2, b.an_w, s));
     BL(gemm(bl, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
-    CK(cfm_attention(m->qkv.p, B, T, d, c.n_heads, m->att.p, s));
+    CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, s));
     BL(gemm(bl, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
     BL(gemm(bl, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));

@@ -217,7 +217,10 @@ hipError_t cfm_add_bias(float *C, int ldc, const float *bias, int rows, int cols
 hipError_t cfm_adaln(const float *x, float *y, int R, int T, int d, const float *mod, int ld_mod, const float *norm_w,
                      hipStream_t s);
 hipError_t cfm_final_norm(const float *x, float *y, int R, int T, int d, const float *mod, hipStream_t s);
-hipError_t cfm_attention(const float *qkv, int B, int T, int d, int H, float *out, hipStream_t s);
+// rope (cos, sin) table [T][32][2] for positions 0..T-1
+hipError_t cfm_rope_table(int T, float *tab, hipStream_t s);
+hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
+                         hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);
 hipError_t cfm_gate(const float *acts, const float *in_b, const float *g, int ld_g, int R, int T, int d, float *act,
                     hipStream_t s);

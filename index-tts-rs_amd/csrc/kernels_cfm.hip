@@ -3,7 +3,7 @@
 // The estimator's linears are plain fp32 GEMMs and run in rocBLAS; the kernels here are
 // the parts around them, fused where a GEMM's output is consumed elementwise: the
 // timestep frequency embedding, AdaLN over RMSNorm (one pass per row), non-causal
-// attention with rope applied while K and Q are staged (no rotated copy in HBM), SwiGLU,
+// MFMA attention with rope applied while K and Q are staged (no rotated copy in HBM), SwiGLU,
 // WaveNet's gated activation and residual / skip accumulation, the final layer norm with
 // its modulation, and the Euler / classifier-free-guidance update.  Activations are
 // [B][T][C] row-major fp32.
@@ -99,110 +99,224 @@ __global__ __launch_bounds__(256) void final_norm_kernel(const float *x, float *
     y[(size_t)r * d + i] = ((xr[i] - mean) * rstd) * (1.0f + scale[i]) + shift[i];
 }
 
-// Non-causal attention (scaled_dot_product_attention, scale 0.125, no mask) of one head over
-// T positions, rope(traditional) applied to Q and K as they are staged (cfm.rs:274-289).
-// qkv [B][T][3d] (q | k | v column blocks), out [B][T][d].  Block: 64 queries of (b, h),
-// 256 threads; thread (q, part) scores keys part*16.. of each 64-key tile and accumulates
-// output dimensions part*16.. .  Online softmax in fp32.
-constexpr int kAq = 64, kAk = 64, kLd = 68;  // LDS row stride keeps 16-byte alignment
-__global__ __launch_bounds__(256) void cfm_attn_kernel(const float *qkv, int T, int d, float *out) {
-  __shared__ __attribute__((aligned(16))) float Ks[kAk * kLd];
-  __shared__ __attribute__((aligned(16))) float Vs[kAk * kLd];
-  __shared__ __attribute__((aligned(16))) float Ps[kAq * kLd];
-  const int b = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * kAq;
-  const int tid = threadIdx.x, qi = tid >> 2, part = tid & 3;
-  const int qpos = q0 + qi;
-  const size_t ld = 3 * (size_t)d;
-  const float *base = qkv + (size_t)b * T * ld;
-  float q[kHd];
+// Rope table (compute_rope_freqs, cfm.rs:73-101): tab[t][k] = (cos, sin) of t * inv_freq(k),
+// k < 32, computed once per sequence length.
+__global__ void rope_table_kernel(int T, float2 *tab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * (kHd / 2)) return;
+  const int t = i / (kHd / 2), k = i % (kHd / 2);
+  const float a = (float)t * rope_inv(k);
+  tab[i] = make_float2(cosf(a), sinf(a));
+}
+
+// Non-causal attention on the MFMA units: scaled_dot_product_attention(scale 0.125, no mask)
+// of one head over T positions, rope(traditional) applied to Q and K as they are staged
+// (cfm.rs:274-289).  qkv [B][T][3d] (q | k | v column blocks) -> out [B][T][d].
+//
+// Block: two waves, 64 query rows of (head, batch); keys in tiles of 64.  Operands are split
+// into fp16 hi/lo planes as they are staged, so S = Qh Kh + Qh Kl + Ql Kh and O += Ph Vh +
+// Ph Vl + Pl Vh run on v_mfma_f32_32x32x16_f16 with ~22-bit operands and fp32 accumulation;
+// online softmax in registers; P reaches the second product's operand layout through a
+// per-wave LDS tile; 16-byte LDS chunks are XOR-swizzled by row.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+constexpr int kAq = 64, kAk = 64;
+
+struct AttnLds {
+  uint16_t k[2][kAk * 64];      // [plane][key][dim]
+  uint16_t vt[2][64 * kAk];     // [plane][dim][key]
+  uint16_t p[2][2][32 * kAk];   // [wave][plane][row][key]
+};
+
+// element offset of 16-byte chunk `chunk` of row `row` in a [row][64] fp16 array
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (row & 7)) << 3); }
+
+__device__ __forceinline__ void split8(const float v[8], u32x4v &hi, u32x4v &lo) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint32_t h0, l0, h1, l1;
+    split_f16(v[2 * j], h0, l0);
+    split_f16(v[2 * j + 1], h1, l1);
+    hi[j] = h0 | (h1 << 16);
+    lo[j] = l0 | (l1 << 16);
+  }
+}
+
+// 8 consecutive values of a head row at dims e0..e0+7 (e0 even), rotated for position t
+__device__ __forceinline__ void load8_rope(const float *p, const float2 *tab, int t, int e0, float v[8]) {
+  const float4 a = *reinterpret_cast<const float4 *>(p);
+  const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+  const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const float2 *tr = tab + (size_t)t * (kHd / 2) + e0 / 2;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float2 cs = tr[j];
+    v[2 * j] = x[2 * j] * cs.x - x[2 * j + 1] * cs.y;
+    v[2 * j + 1] = x[2 * j] * cs.y + x[2 * j + 1] * cs.x;
+  }
+}
+
+__device__ __forceinline__ float half_max32(float v) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float half_sum32(float v) {
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+#define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
+
+__global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const float2 *tab, int T, int d,
+                                                       float *out) {
+  __shared__ AttnLds sh;
+  const int h = blockIdx.x, q0 = blockIdx.y * kAq, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const size_t ld3 = 3 * (size_t)d;
+  const float *base = qkv + (size_t)b * T * ld3;
+
+  // Q fragments of this lane's row (operand layout: row lane & 31, dims kk*16 + (lane>>5)*8 ..)
+  f16x8 qh[4], ql[4];
   {
-    const int qp = qpos < T ? qpos : T - 1;
-    const float *qr = base + (size_t)qp * ld + h * kHd;
+    const int t = min(q0 + w * 32 + (lane & 31), T - 1);
 #pragma unroll
-    for (int k = 0; k < kHd / 2; k++) {
-      const float a = (float)qp * rope_inv(k), c = cosf(a), s = sinf(a);
-      const float x0 = qr[2 * k], x1 = qr[2 * k + 1];
-      q[2 * k] = x0 * c - x1 * s;
-      q[2 * k + 1] = x0 * s + x1 * c;
+    for (int kk = 0; kk < 4; kk++) {
+      const int e0 = kk * 16 + (lane >> 5) * 8;
+      float v[8];
+      load8_rope(base + (size_t)t * ld3 + h * kHd + e0, tab, t, e0, v);
+      u32x4v hi, lo;
+      split8(v, hi, lo);
+      qh[kk] = __builtin_bit_cast(f16x8, hi);
+      ql[kk] = __builtin_bit_cast(f16x8, lo);
     }
   }
-  float m = -INFINITY, l = 0.0f, o[16];
+  float m[16], l[16];
+  floatx16 O[2];
 #pragma unroll
-  for (int e = 0; e < 16; e++) o[e] = 0.0f;
-  for (int k0 = 0; k0 < T; k0 += kAk) {
-    __syncthreads();
-    for (int idx = tid; idx < kAk * (kHd / 2); idx += 256) {
-      const int j = idx / (kHd / 2), k = idx % (kHd / 2), kp = k0 + j;
-      float k0v = 0.0f, k1v = 0.0f, v0 = 0.0f, v1 = 0.0f;
-      if (kp < T) {
-        const float *kr = base + (size_t)kp * ld + d + h * kHd;
-        const float a = (float)kp * rope_inv(k), c = cosf(a), s = sinf(a);
-        const float x0 = kr[2 * k], x1 = kr[2 * k + 1];
-        k0v = x0 * c - x1 * s;
-        k1v = x0 * s + x1 * c;
-        v0 = kr[d + 2 * k];
-        v1 = kr[d + 2 * k + 1];
+  for (int i = 0; i < 16; i++) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+    O[0][i] = 0.0f;
+    O[1][i] = 0.0f;
+  }
+
+  for (int kb = 0; kb < T; kb += kAk) {
+    __syncthreads();  // the previous tile's operands are no longer read
+    {  // K rows (rotated): thread -> key tid/2, dims (tid&1)*32 .. +31
+      const int kr = tid >> 1, key = min(kb + kr, T - 1);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int chunk = (tid & 1) * 4 + c;
+        float v[8];
+        load8_rope(base + (size_t)key * ld3 + d + h * kHd + chunk * 8, tab, key, chunk * 8, v);
+        u32x4v hi, lo;
+        split8(v, hi, lo);
+        *reinterpret_cast<u32x4v *>(&sh.k[0][swz(kr, chunk)]) = hi;
+        *reinterpret_cast<u32x4v *>(&sh.k[1][swz(kr, chunk)]) = lo;
       }
-      Ks[j * kLd + 2 * k] = k0v;
-      Ks[j * kLd + 2 * k + 1] = k1v;
-      Vs[j * kLd + 2 * k] = v0;
-      Vs[j * kLd + 2 * k + 1] = v1;
     }
-    __syncthreads();
-    float s[16], mt = -INFINITY;
+    {  // V transposed: thread -> keys 2kp, 2kp+1, dims (tid&3)*16 .. +15
+      const int kp = tid >> 2;
+      const int k0 = min(kb + 2 * kp, T - 1), k1 = min(kb + 2 * kp + 1, T - 1);
 #pragma unroll
-    for (int jj = 0; jj < 16; jj++) {
-      const int j = part * 16 + jj;
-      const float *kr = Ks + j * kLd;
-      float acc = 0.0f;
+      for (int c = 0; c < 2; c++) {
+        const int e0 = (tid & 3) * 16 + c * 8;
+        const float *va = base + (size_t)k0 * ld3 + 2 * d + h * kHd + e0;
+        const float *vb = base + (size_t)k1 * ld3 + 2 * d + h * kHd + e0;
+        const float4 a0 = *reinterpret_cast<const float4 *>(va), a1 = *reinterpret_cast<const float4 *>(va + 4);
+        const float4 b0 = *reinterpret_cast<const float4 *>(vb), b1 = *reinterpret_cast<const float4 *>(vb + 4);
+        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-      for (int e = 0; e < kHd; e += 4) {
-        const float4 kv = *reinterpret_cast<const float4 *>(kr + e);
-        acc += q[e] * kv.x;
-        acc += q[e + 1] * kv.y;
-        acc += q[e + 2] * kv.z;
-        acc += q[e + 3] * kv.w;
+        for (int j = 0; j < 8; j++) {
+          const int e = e0 + j;
+          uint32_t ha, la, hb2, lb;
+          split_f16(a[j], ha, la);
+          split_f16(bb[j], hb2, lb);
+          const int idx = e * 64 + ((((2 * kp) >> 3) ^ (e & 7)) << 3) + ((2 * kp) & 7);
+          *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
+          *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
+        }
       }
-      s[jj] = k0 + j < T ? acc * 0.125f : -INFINITY;
-      mt = fmaxf(mt, s[jj]);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 1, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 2, 64));
-    const float mn = fmaxf(m, mt);
-    const float alpha = expf(m - mn);
-    float ls = 0.0f;
-#pragma unroll
-    for (int jj = 0; jj < 16; jj++) {
-      const float p = expf(s[jj] - mn);
-      ls += p;
-      Ps[qi * kLd + part * 16 + jj] = p;
-    }
-    ls += __shfl_xor(ls, 1, 64);
-    ls += __shfl_xor(ls, 2, 64);
-    l = l * alpha + ls;
-    m = mn;
-#pragma unroll
-    for (int e = 0; e < 16; e++) o[e] *= alpha;
     __syncthreads();
-    const float *pr = Ps + qi * kLd;
-    for (int j = 0; j < kAk; j++) {
-      const float p = pr[j];
-      const float *vr = Vs + j * kLd + part * 16;
+
+    floatx16 S[2];
 #pragma unroll
-      for (int e = 0; e < 16; e += 4) {
-        const float4 vv = *reinterpret_cast<const float4 *>(vr + e);
-        o[e] += p * vv.x;
-        o[e + 1] += p * vv.y;
-        o[e + 2] += p * vv.z;
-        o[e + 3] += p * vv.w;
+    for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) S[kt][i] = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const int o = swz(kt * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        const f16x8 bh = *reinterpret_cast<const f16x8 *>(&sh.k[0][o]);
+        const f16x8 bl = *reinterpret_cast<const f16x8 *>(&sh.k[1][o]);
+        S[kt] = MFMA16(qh[kk], bh, S[kt], 0, 0, 0);
+        S[kt] = MFMA16(qh[kk], bl, S[kt], 0, 0, 0);
+        S[kt] = MFMA16(ql[kk], bh, S[kt], 0, 0, 0);
+      }
+    }
+
+    uint16_t *pw = sh.p[w][0];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        const int key = kb + kt * 32 + (lane & 31);
+        s[kt] = key >= T ? -INFINITY : S[kt][i] * 0.125f;
+      }
+      const float mn = fmaxf(m[i], half_max32(fmaxf(s[0], s[1])));
+      const float corr = m[i] == -INFINITY ? 1.0f : expf(m[i] - mn);
+      const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      float psum = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        const float p = s[kt] == -INFINITY ? 0.0f : expf(s[kt] - mn);
+        psum += p;
+        uint32_t ph, pl;
+        split_f16(p, ph, pl);
+        const int key = kt * 32 + (lane & 31);
+        const int o = r * 64 + (((key >> 3) ^ (r & 7)) << 3) + (key & 7);
+        pw[o] = (uint16_t)ph;
+        pw[32 * kAk + o] = (uint16_t)pl;
+      }
+      l[i] = l[i] * corr + psum;
+      O[0][i] *= corr;
+      O[1][i] *= corr;
+      m[i] = mn;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's P tile is in LDS
+
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const int oa = swz(lane & 31, kk * 2 + (lane >> 5));
+      const f16x8 ah = *reinterpret_cast<const f16x8 *>(&pw[oa]);
+      const f16x8 al = *reinterpret_cast<const f16x8 *>(&pw[32 * kAk + oa]);
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++) {
+        const int ob = swz(dt * 32 + (lane & 31), kk * 2 + (lane >> 5));
+        const f16x8 bh = *reinterpret_cast<const f16x8 *>(&sh.vt[0][ob]);
+        const f16x8 bl = *reinterpret_cast<const f16x8 *>(&sh.vt[1][ob]);
+        O[dt] = MFMA16(ah, bh, O[dt], 0, 0, 0);
+        O[dt] = MFMA16(ah, bl, O[dt], 0, 0, 0);
+        O[dt] = MFMA16(al, bh, O[dt], 0, 0, 0);
       }
     }
   }
-  if (qpos < T) {
-    float *orow = out + ((size_t)b * T + qpos) * d + h * kHd + part * 16;
-    const float inv = 1.0f / l;
+
 #pragma unroll
-    for (int e = 0; e < 16; e++) orow[e] = o[e] * inv;
+  for (int i = 0; i < 16; i++) {
+    const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+    const float inv = 1.0f / half_sum32(l[i]);
+    if (t < T) {
+      float *orow = out + ((size_t)b * T + t) * d + h * kHd + (lane & 31);
+      orow[0] = O[0][i] * inv;
+      orow[32] = O[1][i] * inv;
+    }
   }
 }
 
@@ -337,9 +451,16 @@ hipError_t cfm_final_norm(const float *x, float *y, int R, int T, int d, const f
   hipLaunchKernelGGL(final_norm_kernel, dim3(R), dim3(256), 0, s, x, y, T, d, mod);
   return hipGetLastError();
 }
-hipError_t cfm_attention(const float *qkv, int B, int T, int d, int H, float *out, hipStream_t s) {
-  if (d != H * kHd) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(cfm_attn_kernel, dim3((T + kAq - 1) / kAq, H, B), dim3(256), 0, s, qkv, T, d, out);
+hipError_t cfm_rope_table(int T, float *tab, hipStream_t s) {
+  hipLaunchKernelGGL(rope_table_kernel, dim3(nblk((long)T * (kHd / 2))), dim3(256), 0, s, T,
+                     reinterpret_cast<float2 *>(tab));
+  return hipGetLastError();
+}
+hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
+                         hipStream_t s) {
+  if (d != H * kHd || T < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(cfm_attn_kernel, dim3(H, (T + kAq - 1) / kAq, B), dim3(128), 0, s, qkv,
+                     reinterpret_cast<const float2 *>(rope_tab), T, d, out);
   return hipGetLastError();
 }
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s) {
