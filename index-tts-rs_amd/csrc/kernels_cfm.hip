@@ -170,10 +170,15 @@ __device__ __forceinline__ float half_sum32(float v) {
 
 #define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
 
-__global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const float2 *tab, int T, int d,
-                                                       float *out) {
+// Keys are split over S blocks per query tile (blockIdx.z = b * S + split, kts key tiles
+// each) so that short sequences still fill the chip; with S > 1 each block writes its
+// unnormalised rows and their (max, denominator) to part_o [S][B][T][d] / part_ml
+// [S][B][H][T][2], combined by attn_combine_kernel.
+__global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const float2 *tab, int T, int d, int S,
+                                                       int kts, float *out, float *part_o, float *part_ml) {
   __shared__ AttnLds sh;
-  const int h = blockIdx.x, q0 = blockIdx.y * kAq, b = blockIdx.z;
+  const int h = blockIdx.x, q0 = blockIdx.y * kAq, b = blockIdx.z / S, sp = blockIdx.z % S;
+  const int B = gridDim.z / S, H = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const size_t ld3 = 3 * (size_t)d;
   const float *base = qkv + (size_t)b * T * ld3;
@@ -203,7 +208,8 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
     O[1][i] = 0.0f;
   }
 
-  for (int kb = 0; kb < T; kb += kAk) {
+  const int kend = min(T, (sp + 1) * kts * kAk);
+  for (int kb = sp * kts * kAk; kb < kend; kb += kAk) {
     __syncthreads();  // the previous tile's operands are no longer read
     {  // K rows (rotated): thread -> key tid/2, dims (tid&1)*32 .. +31
       const int kr = tid >> 1, key = min(kb + kr, T - 1);
@@ -311,13 +317,43 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-    const float inv = 1.0f / half_sum32(l[i]);
+    const float lt = half_sum32(l[i]);
     if (t < T) {
-      float *orow = out + ((size_t)b * T + t) * d + h * kHd + (lane & 31);
-      orow[0] = O[0][i] * inv;
-      orow[32] = O[1][i] * inv;
+      if (S == 1) {
+        float *orow = out + ((size_t)b * T + t) * d + h * kHd + (lane & 31);
+        const float inv = 1.0f / lt;
+        orow[0] = O[0][i] * inv;
+        orow[32] = O[1][i] * inv;
+      } else {
+        float *orow = part_o + (((size_t)sp * B + b) * T + t) * d + h * kHd + (lane & 31);
+        orow[0] = O[0][i];
+        orow[32] = O[1][i];
+        if ((lane & 31) == 0) {
+          float *ml = part_ml + ((((size_t)sp * B + b) * H + h) * T + t) * 2;
+          ml[0] = m[i];
+          ml[1] = lt;
+        }
+      }
     }
   }
+}
+
+// Combines the key splits of cfm_attn_kernel: out = sum_s e^{m_s - M} O_s / sum_s e^{m_s - M} l_s.
+__global__ void attn_combine_kernel(const float *part_o, const float *part_ml, int S, int B, int T, int d,
+                                    float *out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)B * T * d) return;
+  const int c = (int)(i % d), bt = (int)(i / d), b = bt / T, t = bt % T, h = c / kHd, H = d / kHd;
+  float M = -INFINITY;
+  for (int s = 0; s < S; s++) M = fmaxf(M, part_ml[((((size_t)s * B + b) * H + h) * T + t) * 2]);
+  float num = 0.0f, den = 0.0f;
+  for (int s = 0; s < S; s++) {
+    const float *ml = part_ml + ((((size_t)s * B + b) * H + h) * T + t) * 2;
+    const float f = ml[0] == -INFINITY ? 0.0f : expf(ml[0] - M);
+    num += part_o[((size_t)s * B + b) * T * d + (size_t)t * d + c] * f;
+    den += ml[1] * f;
+  }
+  out[i] = num / den;
 }
 
 // SwiGLU (cfm.rs:306-311): out[r][i] = silu(gu[r][i]) * gu[r][F + i]
@@ -456,11 +492,24 @@ hipError_t cfm_rope_table(int T, float *tab, hipStream_t s) {
                      reinterpret_cast<float2 *>(tab));
   return hipGetLastError();
 }
+int cfm_attn_splits(int B, int T, int H) {
+  const int tiles = (T + kAk - 1) / kAk, blocks = H * ((T + kAq - 1) / kAq) * B;
+  int S = (1024 + blocks - 1) / blocks;  // about four blocks of two waves per compute unit
+  S = S < 1 ? 1 : S > 8 ? 8 : S;
+  if (S > tiles) S = tiles;
+  const int kts = (tiles + S - 1) / S;
+  return (tiles + kts - 1) / kts;  // no split without keys
+}
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
-                         hipStream_t s) {
+                         float *part_o, float *part_ml, hipStream_t s) {
   if (d != H * kHd || T < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(cfm_attn_kernel, dim3(H, (T + kAq - 1) / kAq, B), dim3(128), 0, s, qkv,
-                     reinterpret_cast<const float2 *>(rope_tab), T, d, out);
+  const int S = cfm_attn_splits(B, T, H), tiles = (T + kAk - 1) / kAk, kts = (tiles + S - 1) / S;
+  if (S > 1 && (!part_o || !part_ml)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(cfm_attn_kernel, dim3(H, (T + kAq - 1) / kAq, B * S), dim3(128), 0, s, qkv,
+                     reinterpret_cast<const float2 *>(rope_tab), T, d, S, kts, out, part_o, part_ml);
+  if (S > 1)
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(nblk((long)B * T * d)), dim3(256), 0, s, part_o, part_ml, S, B, T, d,
+                       out);
   return hipGetLastError();
 }
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s) {
