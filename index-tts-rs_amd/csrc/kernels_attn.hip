@@ -8,7 +8,8 @@
 // run on v_mfma_f32_32x32x16_f16 with ~22-bit operands and fp32 accumulation.  The
 // softmax is online (running row max and denominator in registers); P goes through a
 // per-wave LDS tile to reach the operand layout of the second product.  16-byte LDS
-// chunks are XOR-swizzled by row so that fragment reads spread over the banks.
+// chunks are XOR-swizzled by (row >> 1) & 7 (a 128-byte row is half of gfx950's 256-byte
+// bank row) so that fragment reads spread over the 64 banks.
 //
 // Query row t sits at cache position base + t and attends to keys ks(t)..base + t, with
 // ks(t) = kstart[t] (concatenated sequences) or 0.
@@ -32,7 +33,7 @@ struct FlashLds {
 };
 
 // element offset of 16-byte chunk `chunk` of row `row` in a [row][64] fp16 array
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (row & 7)) << 3); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 template <int KVT>
 __device__ __forceinline__ void load8(const void *base, size_t idx, float v[8]) {
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
           uint32_t ha, la, hb2, lb;
           split_f16(a[j], ha, la);
           split_f16(b[j], hb2, lb);
-          const int idx = e * 64 + ((((2 * kp) >> 3) ^ (e & 7)) << 3) + ((2 * kp) & 7);
+          const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
           *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
           *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
         }
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
         uint32_t ph, pl;
         split_f16(p, ph, pl);
         const int key = kt * 32 + (lane & 31);
-        const int o = r * 64 + (((key >> 3) ^ (r & 7)) << 3) + (key & 7);
+        const int o = r * 64 + (((key >> 3) ^ ((r >> 1) & 7)) << 3) + (key & 7);
         pw[o] = (uint16_t)ph;
         pw[32 * kFK + o] = (uint16_t)pl;
       }

@@ -130,7 +130,7 @@ struct AttnLds {
 };
 
 // element offset of 16-byte chunk `chunk` of row `row` in a [row][64] fp16 array
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (row & 7)) << 3); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
 __device__ __forceinline__ void split8(const float v[8], u32x4v &hi, u32x4v &lo) {
 #pragma unroll
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
           uint32_t ha, la, hb2, lb;
           split_f16(a[j], ha, la);
           split_f16(bb[j], hb2, lb);
-          const int idx = e * 64 + ((((2 * kp) >> 3) ^ (e & 7)) << 3) + ((2 * kp) & 7);
+          const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
           *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
           *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
         }
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
         uint32_t ph, pl;
         split_f16(p, ph, pl);
         const int key = kt * 32 + (lane & 31);
-        const int o = r * 64 + (((key >> 3) ^ (r & 7)) << 3) + (key & 7);
+        const int o = r * 64 + (((key >> 3) ^ ((r >> 1) & 7)) << 3) + (key & 7);
         pw[o] = (uint16_t)ph;
         pw[32 * kAk + o] = (uint16_t)pl;
       }

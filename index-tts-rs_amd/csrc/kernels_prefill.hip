@@ -46,6 +46,12 @@ struct Shape {
   static_assert(B_BYTES % 1024 == 0 && P_BYTES % 256 == 0, "tile shape");
 };
 
+// LDS on gfx950 has 64 four-byte banks (256 bytes a cycle).  A row of the activation tile
+// is 128 bytes, so rows r and r + 1 share one 256-byte bank row; 16-byte chunks are XOR
+// swizzled by (r >> 1) & 7 so that the 16 rows a wave reads per cycle hit distinct banks.
+// A code row is 64 (8-bit) or 32 (4-bit) bytes; its 16-byte chunks are swizzled by the row's
+// position among the rows sharing a bank row.
+__device__ __forceinline__ int swz_act(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int swz_codes(int bits, int r) { return bits == 8 ? (r >> 2) & 3 : (r >> 3) & 1; }
 
 // two consecutive 8-bit codes (bits sh..sh+15 of w) -> packed fp16 pair (exact)
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
       if (j < Sh::nA) {
         const int plane = j / (BM / 8), c1k = j % (BM / 8);
         const int r = c1k * 8 + (lane >> 3);
-        const int lc = (lane & 7) ^ (r & 7);
+        const int lc = (lane & 7) ^ swz_act(r);
         const int m = min(m0 + r, M - 1);
         const uint16_t *src = (plane ? a.x.lo : a.x.hi) + (size_t)m * K + g * kGroup + lc * 8;
         dma16(src, lds_addr(st + plane * Sh::A_BYTES + c1k * 1024));
@@ -178,45 +184,52 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int e = 0; e < 16; e++) P[i][j][e] = 0.0f;
+    // K order inside a group: lane half h = lane >> 5 of MFMA step kk = 2 kp + s takes the 8
+    // values 32 kp + 16 h + 8 s .. +7 (the same permutation for activations and codes, so
+    // the contraction is unchanged); a lane's codes for both steps of a pair are then one
+    // contiguous 16-byte (8-bit) or 8-byte (4-bit) read.
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-      f16x8 ah[TM], al[TM], bq[TN];
-#pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int row = wm * 32 * TM + i * 32 + (lane & 31);
-        const int c = kk * 2 + (lane >> 5);
-        const int off = row * 128 + ((c ^ (row & 7)) << 4);
-        ah[i] = *reinterpret_cast<const f16x8 *>(st + off);
-        al[i] = *reinterpret_cast<const f16x8 *>(st + Sh::OFF_LO + off);
-      }
+    for (int kp = 0; kp < 2; kp++) {
+      const int h = lane >> 5;
+      f16x8 bq[2][TN];
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const int nr = wn * 32 * TN + j * 32 + (lane & 31);
-        u32x4 bw;
         if constexpr (BITS == 8) {
-          const uint2 q = *reinterpret_cast<const uint2 *>(st + Sh::OFF_B + nr * 64 + ((kk ^ swz_codes(8, nr)) << 4) +
-                                                           (lane >> 5) * 8);
-          bw[0] = f16_pair_u8(q.x, 0);
-          bw[1] = f16_pair_u8(q.x, 16);
-          bw[2] = f16_pair_u8(q.y, 0);
-          bw[3] = f16_pair_u8(q.y, 16);
+          const u32x4 q =
+              *reinterpret_cast<const u32x4 *>(st + Sh::OFF_B + nr * 64 + (((2 * kp + h) ^ swz_codes(8, nr)) << 4));
+          const u32x4 b0 = {f16_pair_u8(q[0], 0), f16_pair_u8(q[0], 16), f16_pair_u8(q[1], 0), f16_pair_u8(q[1], 16)};
+          const u32x4 b1 = {f16_pair_u8(q[2], 0), f16_pair_u8(q[2], 16), f16_pair_u8(q[3], 0), f16_pair_u8(q[3], 16)};
+          bq[0][j] = __builtin_bit_cast(f16x8, b0);
+          bq[1][j] = __builtin_bit_cast(f16x8, b1);
         } else {
-          const uint32_t q = *reinterpret_cast<const uint32_t *>(
-              st + Sh::OFF_B + nr * 32 + (((kk >> 1) ^ swz_codes(4, nr)) << 4) + (kk & 1) * 8 + (lane >> 5) * 4);
-          bw[0] = f16_pair_u4(q, 0);
-          bw[1] = f16_pair_u4(q, 8);
-          bw[2] = f16_pair_u4(q, 16);
-          bw[3] = f16_pair_u4(q, 24);
+          const uint2 q =
+              *reinterpret_cast<const uint2 *>(st + Sh::OFF_B + nr * 32 + ((kp ^ swz_codes(4, nr)) << 4) + h * 8);
+          const u32x4 b0 = {f16_pair_u4(q.x, 0), f16_pair_u4(q.x, 8), f16_pair_u4(q.x, 16), f16_pair_u4(q.x, 24)};
+          const u32x4 b1 = {f16_pair_u4(q.y, 0), f16_pair_u4(q.y, 8), f16_pair_u4(q.y, 16), f16_pair_u4(q.y, 24)};
+          bq[0][j] = __builtin_bit_cast(f16x8, b0);
+          bq[1][j] = __builtin_bit_cast(f16x8, b1);
         }
-        bq[j] = __builtin_bit_cast(f16x8, bw);
       }
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int sub = 0; sub < 2; sub++) {
+        f16x8 ah[TM], al[TM];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-          P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bq[j], P[i][j], 0, 0, 0);
-          P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bq[j], P[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; i++) {
+          const int row = wm * 32 * TM + i * 32 + (lane & 31);
+          const int c = 4 * kp + 2 * h + sub;
+          const int off = row * 128 + ((c ^ swz_act(row)) << 4);
+          ah[i] = *reinterpret_cast<const f16x8 *>(st + off);
+          al[i] = *reinterpret_cast<const f16x8 *>(st + Sh::OFF_LO + off);
         }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bq[sub][j], P[i][j], 0, 0, 0);
+            P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bq[sub][j], P[i][j], 0, 0, 0);
+          }
+      }
     }
   };
 
