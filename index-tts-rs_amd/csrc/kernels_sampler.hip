@@ -1,83 +1,18 @@
-// On-device sampler: sample_next_token (sampler.rs:191-284) in one 1024-thread block.
-//
-// Bit-exactness.  Given the same fp32 logits, this kernel returns the token the
-// reference's algorithm returns: every value-producing operation is the same IEEE
-// operation in the same order (penalty multiply/divide, x * (1/T), the exponential
-// below, the sequential fp32 sums over the sorted candidates, the SplitMix64 draw).
-// Only the top-k selection and sorting are parallel, and they are order-exact: the
-// candidates are ranked by (value desc, index asc) — the total order that pins down
-// the reference's unstable sort on ties.
-//
-// Stages: (1) each thread holds up to 9 consecutive logits in registers, applies the
-// STOP mask (generate mode) and the repetition penalty; (2) greedy: block argmax;
-// (3) otherwise scale by 1/T, radix-select the k-th largest key (4 passes of 8 bits
-// over an order-preserving 32-bit key), take ties at the threshold by lowest index
-// (block prefix scan), bitonic-sort the k candidates in LDS; (4) one thread forms the
-// probabilities' prefix sums, the top-p cut and the draw.
+// On-device sampler: sample_next_token (sampler.rs:191-284) in one 1024-thread block; the
+// algorithm and its bit-exactness argument are in sampler_core.h.
 #include "kernels.h"
-
-// Every multiply and add in this file rounds on its own (no FMA contraction), as the
-// reference's scalar Rust code does; the exponential uses explicit fmaf where intended.
-#pragma clang fp contract(off)
+#include "sampler_core.h"
 
 namespace itts {
 
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kPerThread = 9;  // n <= 9216
+constexpr int kThreads = kSampThreads;
+constexpr int kPerThread = kSampPerThread;
 
-// exp by Cody-Waite reduction with ln2 split and a degree-7 Taylor polynomial in
-// Horner form; results below FLT_MIN flush to +0.
-__device__ inline float sampler_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return INFINITY;
-  if (x < -87.33654022216797f) return 0.0f;
-  const float n = __builtin_rintf(mul_rn(x, 1.44269502162933349609375f));
-  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
-  r = __builtin_fmaf(-n, 1.428606765330187045e-06f, r);
-  float p = 1.98412698412698413e-4f;
-  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
-  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
-  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
-  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
-  p = __builtin_fmaf(p, r, 0.5f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  p = __builtin_fmaf(p, r, 1.0f);
-  const float y = ldexpf(p, (int)n);
-  return y < 1.17549435082228751e-38f ? 0.0f : y;
-}
-
-__device__ inline uint64_t splitmix_next(uint64_t *state) {
-  *state += 0x9E3779B97F4A7C15ull;
-  uint64_t z = *state;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
-__device__ inline bool is_finite(float v) { return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u; }
-
-// Order-preserving key of a non-NaN float, with -0 == +0.
-__device__ inline uint32_t order_key(float v) {
-  uint32_t u = __float_as_uint(v);
-  if ((u & 0x7fffffffu) == 0) u = 0;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ inline float key_value(uint32_t k) {
-  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __uint_as_float(u);
-}
-
-struct SamplerShared {
-  uint32_t hist[256];
-  int32_t wave_tot[kThreads / 64];
-  int32_t scal[8];
-  float fred[kThreads / 64];
-  int32_t ired[kThreads / 64];
-};
-
+// mode 0: API call on `logits` (penalised in place, token to *tok_out, rng advanced);
+// mode 1: generate step driven by ctl (seen, rng, min_codes, bookkeeping); batch mode
+// (seqs != nullptr): block b serves sequence b with its own logits row, ctl and params.
 __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n, const uint64_t *seen_in,
                                                            DevSampling p, uint64_t *rng_in,
                                                            int32_t *tok_out, DecodeCtl *ctl,
@@ -85,7 +20,7 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
                                                            const DevSampling *ps, const BatchSeq *seqs) {
   __shared__ SamplerShared sh;
   extern __shared__ uint64_t sk[];  // [P] sort keys
-  if (seqs != nullptr) {  // batch: block b serves sequence b
+  if (seqs != nullptr) {
     ctl = seqs[blockIdx.x].ctl;
     codes = seqs[blockIdx.x].codes;
     p = ps[blockIdx.x];
@@ -94,250 +29,13 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
   if (mode == 1 && ctl->done) return;
   const uint64_t *seen = mode == 1 ? ctl->seen : seen_in;
   uint64_t *rng = mode == 1 ? &ctl->rng : rng_in;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int E = (n + kThreads - 1) / kThreads;
-  const int i0 = tid * E;
   const bool mask_stop = mode == 1 && ctl->n_codes < ctl->min_codes;
-
-  // (1) load, STOP mask, repetition penalty (x<0 ? x*p : x/p)
-  float v[kPerThread];
-#pragma unroll
-  for (int e = 0; e < kPerThread; e++) {
-    const int i = i0 + e;
-    float x = 0.0f;
-    if (e < E && i < n) {
-      x = logits[i];
-      if (mask_stop && i == stop_tok) x = -INFINITY;
-      if (p.apply_penalty && (i >> 6) < kSeenWords && ((seen[i >> 6] >> (i & 63)) & 1ull)) {
-        x = x < 0.0f ? mul_rn(x, p.penalty) : div_rn(x, p.penalty);
-      }
-      if (mode == 0) logits[i] = x;
-    }
-    v[e] = x;
-  }
-
-  int32_t result = 0;
-  if (p.greedy) {
-    // (2) first index of the strict maximum over finite values; 0 if none is finite.
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int i = i0 + e;
-      if (e < E && i < n && is_finite(v[e]) && v[e] > bv) {
-        bv = v[e];
-        bi = i;
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (lane == 0) {
-      sh.fred[wave] = bv;
-      sh.ired[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float gv = -INFINITY;
-      int gi = 0x7fffffff;
-      for (int w = 0; w < kThreads / 64; w++) {
-        if (sh.fred[w] > gv || (sh.fred[w] == gv && sh.ired[w] < gi)) {
-          gv = sh.fred[w];
-          gi = sh.ired[w];
-        }
-      }
-      sh.scal[0] = gi == 0x7fffffff ? 0 : gi;
-    }
-    __syncthreads();
-    result = sh.scal[0];
-  } else {
-    // (3) temperature, then keys
-    uint32_t key[kPerThread];
-#pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int i = i0 + e;
-      const bool live = e < E && i < n;
-      const float s = is_finite(v[e]) ? mul_rn(v[e], p.inv_temp) : -INFINITY;
-      v[e] = s;
-      key[e] = live ? order_key(s) : 0u;  // padding sorts below -inf (key 0x007fffff)
-    }
-    const int k = p.top_k;
-    // radix select of the k-th largest key
-    uint32_t prefix = 0, pmask = 0;
-    int remaining = k;
-    for (int pass = 0; pass < 4; pass++) {
-      const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += kThreads) sh.hist[b] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int e = 0; e < kPerThread; e++) {
-        const int i = i0 + e;
-        if (e < E && i < n && (key[e] & pmask) == prefix) atomicAdd(&sh.hist[(key[e] >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (wave == 0) {
-        // lane l covers bins 255-4l .. 252-4l (descending)
-        uint32_t c[4];
-        uint32_t tot = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          c[j] = sh.hist[255 - 4 * lane - j];
-          tot += c[j];
-        }
-        uint32_t incl = tot;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t o = __shfl_up(incl, off, 64);
-          if (lane >= off) incl += o;
-        }
-        uint32_t above = incl - tot;  // elements in strictly higher bins
-        if (above < (uint32_t)remaining && (uint32_t)remaining <= incl) {
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            if (above < (uint32_t)remaining && (uint32_t)remaining <= above + c[j]) {
-              sh.scal[0] = 255 - 4 * lane - j;
-              sh.scal[1] = (int)above;
-            }
-            above += c[j];
-          }
-        }
-      }
-      __syncthreads();
-      const uint32_t digit = (uint32_t)sh.scal[0];
-      remaining -= sh.scal[1];
-      prefix |= digit << shift;
-      pmask |= 0xffu << shift;
-      __syncthreads();
-    }
-    const uint32_t thr = prefix;  // key of the k-th largest; `remaining` ties to take
-    // ties at the threshold: take the `remaining` lowest indices (prefix scan in index order)
-    int my_eq = 0;
-#pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int i = i0 + e;
-      if (e < E && i < n && key[e] == thr) my_eq++;
-    }
-    int incl = my_eq;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int o = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += o;
-    }
-    if (lane == 63) sh.wave_tot[wave] = incl;
-    if (tid == 0) sh.scal[2] = 0;  // candidate counter
-    __syncthreads();
-    int eq_before = incl - my_eq;
-    for (int w = 0; w < wave; w++) eq_before += sh.wave_tot[w];
-    const int P = (int)next_pow2((uint32_t)k);
-#pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int i = i0 + e;
-      if (!(e < E && i < n)) continue;
-      bool take = key[e] > thr;
-      if (key[e] == thr) {
-        take = eq_before < remaining;
-        eq_before++;
-      }
-      if (take) {
-        const int slot = atomicAdd(&sh.scal[2], 1);
-        if (slot < k) sk[slot] = ((uint64_t)key[e] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
-      }
-    }
-    __syncthreads();
-    for (int i = k + tid; i < P; i += kThreads) sk[i] = 0ull;
-    __syncthreads();
-    // bitonic sort, descending
-    for (int size = 2; size <= P; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = tid; t < P / 2; t += kThreads) {
-          const int i = 2 * t - (t & (stride - 1));
-          const int j = i + stride;
-          const bool desc = (i & size) == 0;
-          const uint64_t x = sk[i], y = sk[j];
-          if ((x < y) == desc) {
-            sk[i] = y;
-            sk[j] = x;
-          }
-        }
-        __syncthreads();
-      }
-    }
-    // (4) probabilities p_i = exp(v_i - max); repack as (p bits << 32 | id)
-    const float v0 = key_value((uint32_t)(sk[0] >> 32));
-    const float mx = is_finite(v0) ? v0 : 0.0f;
-    for (int i = tid; i < k; i += kThreads) {
-      const uint64_t e = sk[i];
-      const float vi = key_value((uint32_t)(e >> 32));
-      const uint32_t id = 0xffffffffu - (uint32_t)e;
-      const float pi = is_finite(vi) ? sampler_expf(sub_rn(vi, mx)) : 0.0f;
-      sk[i] = ((uint64_t)__float_as_uint(pi) << 32) | id;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float prob_sum = 0.0f;
-      for (int i = 0; i < k; i++) prob_sum = add_rn(prob_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
-      int32_t tok = (int32_t)(uint32_t)sk[0];
-      if (prob_sum > 0.0f && is_finite(prob_sum)) {
-        float cum = 0.0f;
-        int active = k;
-        for (int i = 0; i < k; i++) {
-          const float norm = div_rn(__uint_as_float((uint32_t)(sk[i] >> 32)), prob_sum);
-          if (i > 0 && cum > p.top_p) {
-            active = i;
-            break;
-          }
-          cum = add_rn(cum, norm);
-        }
-        float active_sum = 0.0f;
-        for (int i = 0; i < active; i++) active_sum = add_rn(active_sum, __uint_as_float((uint32_t)(sk[i] >> 32)));
-        if (active_sum > 0.0f && is_finite(active_sum)) {
-          const uint32_t upper = (uint32_t)(splitmix_next(rng) >> 40);
-          const float u = mul_rn((float)upper, 1.0f / 16777216.0f);
-          const float draw = mul_rn(u, active_sum);
-          float accp = 0.0f;
-          tok = (int32_t)(uint32_t)sk[active - 1];
-          for (int i = 0; i < active; i++) {
-            accp = add_rn(accp, __uint_as_float((uint32_t)(sk[i] >> 32)));
-            if (draw <= accp) {
-              tok = (int32_t)(uint32_t)sk[i];
-              break;
-            }
-          }
-        }
-      }
-      sh.scal[3] = tok;
-    }
-    __syncthreads();
-    result = sh.scal[3];
-  }
-
-  if (tid == 0) {
-    if (mode == 0) {
+  const int32_t result = sample_block(logits, mode == 0 ? logits : nullptr, n, seen, p, rng, mask_stop, stop_tok, sh, sk);
+  if (threadIdx.x == 0) {
+    if (mode == 0)
       *tok_out = result;
-    } else {
-      ctl->last_tok = result;
-      if (result == stop_tok) {
-        ctl->done = 1;
-      } else {
-        codes[ctl->n_codes] = result;
-        ctl->n_codes += 1;
-        if (result >= 0 && result < kSeenWords * 64) ctl->seen[result >> 6] |= 1ull << (result & 63);
-        const int s = ctl->step;
-        if (s + 1 < ctl->max_steps) {
-          ctl->tok = result;
-          ctl->pos = ctl->n_prior + s + 2;
-        } else {
-          ctl->done = 1;
-        }
-      }
-      ctl->step += 1;
-    }
+    else
+      sampler_commit(ctl, ctl->seen, result, stop_tok, codes);
   }
 }
 

@@ -97,7 +97,8 @@ for kind in ("normal", "ties", "special", "raw"):
     for greedy, k, p_, t, pen in [(True, 3, 0.8, 0.8, 10.0), (False, 30, 0.8, 0.8, 10.0),
                                   (False, 3, 0.8, 0.8, 10.0), (False, 1, 0.5, 1.0, 1.0),
                                   (False, 500, 0.95, 1.3, 2.0), (False, 0, 1.0, 0.7, 1.5),
-                                  (False, 8194, 0.3, 0.05, 50.0), (False, 4096, 0.9, 2.0, 1.0)]:
+                                  (False, 8194, 0.3, 0.05, 50.0), (False, 4096, 0.9, 2.0, 1.0),
+                                  (False, 64, 0.9, 0.8, 10.0), (False, 33, 0.99, 1.0, 1.0), (False, 65, 0.9, 0.8, 2.0)]:
         CASES.append((kind, greedy, k, p_, t, pen))
 
 
