@@ -136,6 +136,36 @@ __device__ inline float wave_max(float v) {
   return v;
 }
 
+// Reductions over each 32-lane half of a wave (lanes 0-31 and 32-63), result in every lane
+// of the half.  Every step pairs lane i with a partner that pairs back with i (xor 1 and
+// xor 2 within a quad, the 8-lane and 16-lane mirrors, then lane i ^ 16), so both lanes of
+// a pair form the same value (a + b == b + a) and the half ends with one bit-identical
+// result.  Four steps are DPP moves (VALU, no LDS round trip) and the last a ds_swizzle,
+// so independent reductions overlap instead of waiting on five LDS permutes each.  Every
+// lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_pair(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  // bitmask mode: and 0x1f, or 0, xor 0x10 within each group of 32 lanes
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+}
+__device__ __forceinline__ float half32_max(float v) {
+  v = fmaxf(v, dpp_pair<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_pair<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_pair<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_pair<0x140>(v));  // row_mirror
+  return fmaxf(v, swizzle_xor16(v));
+}
+__device__ __forceinline__ float half32_sum(float v) {
+  v += dpp_pair<0xB1>(v);
+  v += dpp_pair<0x4E>(v);
+  v += dpp_pair<0x141>(v);
+  v += dpp_pair<0x140>(v);
+  return v + swizzle_xor16(v);
+}
+
 // gelu_approximate (tanh form).
 __device__ inline float gelu_tanh(float x) {
   const float x3 = x * x * x;

@@ -63,17 +63,6 @@ __device__ __forceinline__ void split8(const float v[8], u32x4 &hi, u32x4 &lo) {
   }
 }
 
-__device__ __forceinline__ float half_max32(float v) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float half_sum32(float v) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 #define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
 
 template <int KVT>
@@ -179,16 +168,23 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
       }
     }
 
-    uint16_t *pw = sh.p[w][0];
+    // masked, scaled scores and the 16 row maxima of the tile (independent reductions,
+    // issued together)
+    float tmax[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      float s[2];
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
         const int key = kb + kt * 32 + (lane & 31);
-        s[kt] = (key > pos[i] || key < ks[i]) ? -INFINITY : S[kt][i] * 0.125f;
+        S[kt][i] = (key > pos[i] || key < ks[i]) ? -INFINITY : S[kt][i] * 0.125f;
       }
-      const float mn = fmaxf(m[i], half_max32(fmaxf(s[0], s[1])));
+      tmax[i] = half32_max(fmaxf(S[0][i], S[1][i]));
+    }
+    uint16_t *pw = sh.p[w][0];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float s[2] = {S[0][i], S[1][i]};
+      const float mn = fmaxf(m[i], tmax[i]);
       const float corr = m[i] == -INFINITY ? 1.0f : __expf(m[i] - mn);
       const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
       float psum = 0.0f;
@@ -231,9 +227,9 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-    const float inv = 1.0f / half_sum32(l[i]);
+    const float inv = 1.0f / half32_sum(l[i]);
     const float v0 = O[0][i] * inv, v1 = O[1][i] * inv;
-    const float gsum = half_sum32(v0 + v1);
+    const float gsum = half32_sum(v0 + v1);
     if (t < T) {
       const size_t row = (size_t)t * d + h * 64 + (lane & 31);
       uint32_t hi, lo;

@@ -157,17 +157,6 @@ __device__ __forceinline__ void load8_rope(const float *p, const float2 *tab, in
   }
 }
 
-__device__ __forceinline__ float half_max32(float v) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float half_sum32(float v) {
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 #define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
 
 // Keys are split over S blocks per query tile (blockIdx.z = b * S + split, kts key tiles
@@ -266,16 +255,23 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
       }
     }
 
-    uint16_t *pw = sh.p[w][0];
+    // masked, scaled scores and the 16 row maxima of the tile (independent reductions,
+    // issued together)
+    float tmax[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      float s[2];
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
         const int key = kb + kt * 32 + (lane & 31);
-        s[kt] = key >= T ? -INFINITY : S[kt][i] * 0.125f;
+        S[kt][i] = key >= T ? -INFINITY : S[kt][i] * 0.125f;
       }
-      const float mn = fmaxf(m[i], half_max32(fmaxf(s[0], s[1])));
+      tmax[i] = half32_max(fmaxf(S[0][i], S[1][i]));
+    }
+    uint16_t *pw = sh.p[w][0];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float s[2] = {S[0][i], S[1][i]};
+      const float mn = fmaxf(m[i], tmax[i]);
       const float corr = m[i] == -INFINITY ? 1.0f : expf(m[i] - mn);
       const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
       float psum = 0.0f;
@@ -317,7 +313,7 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
 #pragma unroll
   for (int i = 0; i < 16; i++) {
     const int t = q0 + w * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-    const float lt = half_sum32(l[i]);
+    const float lt = half32_sum(l[i]);
     if (t < T) {
       if (S == 1) {
         float *orow = out + ((size_t)b * T + t) * d + h * kHd + (lane & 31);

@@ -508,15 +508,28 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
   p.mt = (a.M + BM - 1) / BM;
   const int tiles = p.nN * p.mt;
   const int slots = std::max(1, a.n_cu) * (large ? 1 : 2);
-  // fewest rounds x groups per split, with a fixed cost for the fill and a split
-  // reduction; partial tiles must fit the workspace
-  int bestS = 1, best = 1 << 30;
+  // Split count with the lowest modelled time; partial tiles must fit the workspace.
+  // Small tiles (two blocks per CU), in microseconds, fitted to MI355X timings of the
+  // decoder's four GEMM shapes at 99 and 235 rows: a block takes ~0.67 us per K group;
+  // a second round of blocks costs ~6.7 us; a split-K reduction ~3.2 us plus ~0.64 us per
+  // split (the last block of a tile adds every partial).  Large tiles (one block per CU):
+  // rounds x (groups + fill) in group units plus a reduction term.
+  int bestS = 1;
+  double best = 1e30;
   for (int S = 1; S <= std::min(G, 32); S++) {
     const int gps = (G + S - 1) / S, Se = (G + gps - 1) / gps;
     if (Se != S) continue;
     if (S > 1 && ((size_t)tiles * S * BM * BN > a.ws_floats || tiles > a.cnt_words)) break;
-    const int rounds = (tiles * S + slots - 1) / slots;
-    const int cost = rounds * (gps + 3) + (S > 1 ? 2 : 0);
+    const int blocks = tiles * S;
+    const int rounds = (blocks + slots - 1) / slots;
+    double cost;
+    if (large) {
+      cost = rounds * (gps + 3) + (S > 1 ? 2 : 0);
+    } else {
+      const double per_cu = (double)std::min(blocks, slots) / std::max(1, a.n_cu);
+      cost = 0.674 * rounds * gps - 0.091 * rounds * gps * std::max(0.0, per_cu - 1.0) +
+             (S > 1 ? 3.2 : 0.0) + 0.636 * S + 6.65 * (rounds - 1);
+    }
     if (cost < best) {
       best = cost;
       bestS = S;
