@@ -165,6 +165,18 @@ __device__ __forceinline__ float half32_sum(float v) {
   v += dpp_pair<0x140>(v);
   return v + swizzle_xor16(v);
 }
+// Whole-wave versions: the two half results combined as wave-uniform scalars.
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ float wave64_max_dpp(float v) {
+  v = half32_max(v);
+  return fmaxf(lane_value(v, 0), lane_value(v, 32));
+}
+__device__ __forceinline__ float wave64_sum_dpp(float v) {
+  v = half32_sum(v);
+  return lane_value(v, 0) + lane_value(v, 32);
+}
 
 // gelu_approximate (tanh form).
 __device__ inline float gelu_tanh(float x) {

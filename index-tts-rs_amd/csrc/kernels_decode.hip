@@ -490,11 +490,14 @@ __global__ void advance_batch_kernel(const BatchSeq *seqs, int B) {
   if (b < B && !seqs[b].ctl->done) seqs[b].ctl->valid_len += 1;
 }
 
-// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows).
+// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows).  Scores:
+// lane = key of the 64-key tile.  Values: lane = (key group kg = lane / 8, dims 8 (lane % 8)
+// .. +7); a lane accumulates keys kg, kg + 8, .. of every tile with one 16-byte load each,
+// and the eight key groups are added once at the end.  o returns dimension `lane`.
 template <int KVT>
 __device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
                                   float &m, float &l, float &o, float *p_lds) {
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
   float qr[64];
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -506,7 +509,9 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
   }
   m = -INFINITY;
   l = 0.0f;
-  o = 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = 0.0f;
   for (int t0 = j0; t0 < j1; t0 += 64) {
     const int j = t0 + lane;
     float sc = -INFINITY;
@@ -518,23 +523,43 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
       for (int e = 0; e < 64; e++) dot += qr[e] * kr[e];
       sc = dot * 0.125f;
     }
-    const float mt = wave_max(sc);
+    const float mt = wave64_max_dpp(sc);
     const float mn = fmaxf(m, mt);
     const float p = (j < j1) ? __expf(sc - mn) : 0.0f;
     const float corr = (m == -INFINITY) ? 0.0f : __expf(m - mn);
-    l = l * corr + wave_sum(p);
+    l = l * corr + wave64_sum_dpp(p);
     p_lds[lane] = p;
     __syncthreads();
-    o *= corr;
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] *= corr;
     const int cnt = min(64, j1 - t0);
-    for (int jj = 0; jj < cnt; jj++) {
-      const size_t idx = (size_t)(t0 + jj) * 64 + lane;
-      const float v = KVT == kKvBf16 ? __uint_as_float((uint32_t) static_cast<const uint16_t *>(vh)[idx] << 16)
-                                     : static_cast<const float *>(vh)[idx];
-      o += p_lds[jj] * v;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int kk = kg + 8 * jj;
+      if (kk < cnt) {
+        float v[8];
+        load_row8<KVT>(vh, (size_t)(t0 + kk), dc * 8, v);
+        const float pk = p_lds[kk];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] += pk * v[e];
+      }
     }
     __syncthreads();
     m = mn;
+  }
+  // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits in
+  // element lane % 8 of lane lane / 8
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    acc[e] += __shfl_xor(acc[e], 8, 64);
+    acc[e] += __shfl_xor(acc[e], 16, 64);
+    acc[e] += __shfl_xor(acc[e], 32, 64);
+  }
+  o = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = __shfl(acc[e], lane >> 3, 64);
+    if (dc == e) o = x;
   }
 }
 

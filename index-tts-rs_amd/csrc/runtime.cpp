@@ -265,7 +265,7 @@ DevSampling to_dev_sampling(const itts_sampling &p, int n) {
 
 // Prompts up to this many rows use the per-row attention kernel, longer ones the MFMA
 // flash kernel (measured crossover on MI355X at 24 layers x 20 heads).
-constexpr int kFlashMinRows = 320;
+constexpr int kFlashMinRows = 384;
 
 // GEMM arguments over M rows with the decoder's split-K workspace.
 GemmArgs gemm_args(const itts_gpt *g, const DevQL &ql, SplitAct x, int M) {
