@@ -88,15 +88,21 @@ struct Tile {
   int tn, tm, ks;
 };
 
-template <int BITS, int PT, int EPI, int KVT, int TM, int TN, int NS>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN, int mt, int S, int gps) {
+// PROD: 512 threads, waves 4-7 issue every copy and waves 0-3 only compute, so that the
+// copies (bound by the CU's vector-memory path) overlap the MFMA and VALU work instead of
+// running in series with it inside each wave.
+template <int BITS, int PT, int EPI, int KVT, int TM, int TN, int NS, bool PROD>
+__global__ __launch_bounds__(PROD ? 512 : 256) void gemm_kernel(GemmArgs a, int mode, int nN, int mt, int S, int gps) {
   using Sh = Shape<BITS, PT, TM, TN>;
   constexpr int BM = Sh::BM, BN = Sh::BN, PW = Sh::PW;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // copier: issues the copies; worker: computes (both, without PROD).  Wave-uniform.
+  const bool copier = !PROD || wave_all >= 4, worker = !PROD || wave_all < 4;
+  const int wave = wave_all & 3;
   const int wm = wave >> 1, wn = wave & 1;
   const int K = a.ql.K, N = a.ql.N, M = a.M, G = K / kGroup;
 
@@ -272,22 +278,35 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
   // group i-1 used, contract, then fold group i-1's partial (its params were read into
   // registers while the buffer was still valid)
   auto step = [&](int i, floatx16(&Pc)[TM][TN], const floatx16(&Pp)[TM][TN]) __attribute__((always_inline)) {
-    const int ahead = min(NS - 2, ng - 1 - i);
-    if (ahead <= 0) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else if (ahead == 1) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PW) : "memory");
+    if (copier) {
+      const int ahead = min(NS - 2, ng - 1 - i);
+      if (ahead <= 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      } else if (ahead == 1) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PW) : "memory");
+      }
     }
     __syncthreads();
-    if (i + NS - 1 < ng) issue(g0 + i + NS - 1, stage(i + NS - 1));
-    mma(stage(i), Pc);
-    if (i > 0) apply(Pp);
-    read_group(stage(i));
+    if (copier && i + NS - 1 < ng) issue(g0 + i + NS - 1, stage(i + NS - 1));
+    if (worker) {
+      if constexpr (PROD) {
+        // 128 x 128 tiles at two waves per SIMD: the group's affine is applied at once, so
+        // only one partial tile is live (the other wave on the SIMD covers the MFMA latency)
+        mma(stage(i), Pc);
+        read_group(stage(i));
+        apply(Pc);
+      } else {
+        mma(stage(i), Pc);
+        if (i > 0) apply(Pp);
+        read_group(stage(i));
+      }
+    }
   };
 
-  for (int i = 0; i < NS - 1 && i < ng; i++) issue(g0 + i, stage(i));
+  if (copier)
+    for (int i = 0; i < NS - 1 && i < ng; i++) issue(g0 + i, stage(i));
   int i = 0;
   for (; i + 1 < ng; i += 2) {
     step(i, P0, P1);
@@ -295,9 +314,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
   }
   if (i < ng) {
     step(i, P0, P1);
-    apply(P0);
+    if (worker && !PROD) apply(P0);
   } else {
-    apply(P1);
+    if (worker && !PROD) apply(P1);
   }
 
   const int tile = t.tm * nN + t.tn;
@@ -310,46 +329,50 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
     constexpr int TILE = BM * BN;
     uint64_t *wsb = reinterpret_cast<uint64_t *>(a.ws + (size_t)tile * S * TILE);
     uint64_t *mine = wsb + (size_t)t.ks * (TILE / 2);
+    if (worker) {
 #pragma unroll
-    for (int i2 = 0; i2 < TM; i2++)
+      for (int i2 = 0; i2 < TM; i2++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+        for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int h = 0; h < 8; h++) {
-          const float2 v = make_float2(acc[i2][j][2 * h], acc[i2][j][2 * h + 1]);
-          __hip_atomic_store(mine + ((((wave * TM + i2) * TN + j) * 8 + h) * 64 + lane),
-                             __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+          for (int h = 0; h < 8; h++) {
+            const float2 v = make_float2(acc[i2][j][2 * h], acc[i2][j][2 * h + 1]);
+            __hip_atomic_store(mine + ((((wave * TM + i2) * TN + j) * 8 + h) * 64 + lane),
+                               __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) last_flag = atomicInc(a.cnt + tile, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
     __syncthreads();
     if (!last_flag) return;
     // splits added in split order (the block's own partial from registers)
+    if (worker) {
 #pragma unroll
-    for (int i2 = 0; i2 < TM; i2++)
+      for (int i2 = 0; i2 < TM; i2++)
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const size_t base = (size_t)(((wave * TM + i2) * TN + j) * 8) * 64 + lane;
-        floatx16 sum;
-        for (int s2 = 0; s2 < S; s2++) {
-          floatx16 v;
-          if (s2 == t.ks) {
-            v = acc[i2][j];
-          } else {
+        for (int j = 0; j < TN; j++) {
+          const size_t base = (size_t)(((wave * TM + i2) * TN + j) * 8) * 64 + lane;
+          floatx16 sum;
+          for (int s2 = 0; s2 < S; s2++) {
+            floatx16 v;
+            if (s2 == t.ks) {
+              v = acc[i2][j];
+            } else {
 #pragma unroll
-            for (int h = 0; h < 8; h++) {
-              const float2 w = __builtin_bit_cast(
-                  float2, __hip_atomic_load(wsb + (size_t)s2 * (TILE / 2) + base + h * 64, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT));
-              v[2 * h] = w.x;
-              v[2 * h + 1] = w.y;
+              for (int h = 0; h < 8; h++) {
+                const float2 w = __builtin_bit_cast(
+                    float2, __hip_atomic_load(wsb + (size_t)s2 * (TILE / 2) + base + h * 64, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT));
+                v[2 * h] = w.x;
+                v[2 * h + 1] = w.y;
+              }
             }
+            sum = s2 == 0 ? v : sum + v;
           }
-          sum = s2 == 0 ? v : sum + v;
+          acc[i2][j] = sum;
         }
-        acc[i2][j] = sum;
-      }
+    }
   }
 
   if constexpr (EPI == kEpiGelu) {
@@ -358,6 +381,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
     constexpr int LDT = BN + 1;
     float *T = reinterpret_cast<float *>(lds);
     __syncthreads();
+    if (worker)
 #pragma unroll
     for (int i2 = 0; i2 < TM; i2++)
 #pragma unroll
@@ -373,36 +397,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a, int mode, int nN,
     __syncthreads();
     constexpr int GPR = BN / 64, ITEMS = BM * GPR, TPI = 256 / ITEMS, VPT = 64 / TPI;
     static_assert(ITEMS * TPI == 256 && VPT % 8 == 0, "gelu epilogue shape");
-    const int item = tid / TPI, sub = tid % TPI;
-    const int rl = item / GPR, grp = item % GPR;
-    const int c0 = grp * 64 + sub * VPT;
-    const int m = m0 + rl, n = n0 + c0;
-    float sum = 0.0f;
-    const bool live = m < M && n < N;
+    if (worker) {
+      const int item = tid / TPI, sub = tid % TPI;
+      const int rl = item / GPR, grp = item % GPR;
+      const int c0 = grp * 64 + sub * VPT;
+      const int m = m0 + rl, n = n0 + c0;
+      float sum = 0.0f;
+      const bool live = m < M && n < N;
 #pragma unroll
-    for (int c = 0; c < VPT; c += 8) {
-      uint32_t hw[4], lw[4];
+      for (int c = 0; c < VPT; c += 8) {
+        uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float v0 = T[rl * LDT + c0 + c + e], v1 = T[rl * LDT + c0 + c + e + 1];
-        sum += v0;
-        sum += v1;
-        uint32_t h0, l0, h1, l1;
-        split_f16(v0, h0, l0);
-        split_f16(v1, h1, l1);
-        hw[e >> 1] = h0 | (h1 << 16);
-        lw[e >> 1] = l0 | (l1 << 16);
+        for (int e = 0; e < 8; e += 2) {
+          const float v0 = T[rl * LDT + c0 + c + e], v1 = T[rl * LDT + c0 + c + e + 1];
+          sum += v0;
+          sum += v1;
+          uint32_t h0, l0, h1, l1;
+          split_f16(v0, h0, l0);
+          split_f16(v1, h1, l1);
+          hw[e >> 1] = h0 | (h1 << 16);
+          lw[e >> 1] = l0 | (l1 << 16);
+        }
+        if (live) {
+          *reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+          *reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
       }
-      if (live) {
-        *reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      }
+#pragma unroll
+      for (int o = 1; o < TPI; o <<= 1) sum += __shfl_xor(sum, o, 64);
+      if (live && sub == 0) a.xo.gs[(size_t)m * (N / kGroup) + n / kGroup] = sum;
     }
-#pragma unroll
-    for (int o = 1; o < TPI; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    if (live && sub == 0) a.xo.gs[(size_t)m * (N / kGroup) + n / kGroup] = sum;
     return;
-  } else {
+  } else if (worker) {
 #pragma unroll
     for (int i2 = 0; i2 < TM; i2++)
 #pragma unroll
@@ -546,15 +572,17 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
 
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
 hipError_t set_cfg_attr() {
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages>),
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages, (TM > 1)>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes<BITS, PT, TM, TN>());
 }
 
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
 hipError_t launch_cfg(const GemmArgs &a, const Plan &p, hipStream_t s) {
-  auto *fn = gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages>;
+  // large tiles (one block per CU) run with copier waves; small tiles keep two blocks per CU
+  constexpr bool prod = TM > 1;
+  auto *fn = gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages, prod>;
   constexpr size_t lds = lds_bytes<BITS, PT, TM, TN>();
-  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(256), lds, s, a, p.mode, p.nN, p.mt, p.S, p.gps);
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(prod ? 512 : 256), lds, s, a, p.mode, p.nN, p.mt, p.S, p.gps);
   return hipGetLastError();
 }
 
