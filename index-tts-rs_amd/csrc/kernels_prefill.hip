@@ -92,7 +92,7 @@ struct Tile {
 // copies (bound by the CU's vector-memory path) overlap the MFMA and VALU work instead of
 // running in series with it inside each wave.
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN, int NS, bool PROD>
-__global__ __launch_bounds__(PROD ? 512 : 256) void gemm_kernel(GemmArgs a, int mode, int nN, int mt, int S, int gps) {
+__global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void gemm_kernel(GemmArgs a, int mode, int nN, int mt, int S, int gps) {
   using Sh = Shape<BITS, PT, TM, TN>;
   constexpr int BM = Sh::BM, BN = Sh::BN, PW = Sh::PW;
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -572,14 +572,14 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
 
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
 hipError_t set_cfg_attr() {
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages, (TM > 1)>),
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages, true>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes<BITS, PT, TM, TN>());
 }
 
 template <int BITS, int PT, int EPI, int KVT, int TM, int TN>
 hipError_t launch_cfg(const GemmArgs &a, const Plan &p, hipStream_t s) {
   // large tiles (one block per CU) run with copier waves; small tiles keep two blocks per CU
-  constexpr bool prod = TM > 1;
+  constexpr bool prod = true;
   auto *fn = gemm_kernel<BITS, PT, EPI, KVT, TM, TN, kStages, prod>;
   constexpr size_t lds = lds_bytes<BITS, PT, TM, TN>();
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(prod ? 512 : 256), lds, s, a, p.mode, p.nN, p.mt, p.S, p.gps);
