@@ -535,10 +535,10 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
   const int tiles = p.nN * p.mt;
   const int slots = std::max(1, a.n_cu) * (large ? 1 : 2);
   // Split count with the lowest modelled time; partial tiles must fit the workspace.
-  // Small tiles (two blocks per CU), in microseconds, fitted to MI355X timings of the
-  // decoder's four GEMM shapes at 99 and 235 rows: a block takes ~0.67 us per K group;
-  // a second round of blocks costs ~6.7 us; a split-K reduction ~3.2 us plus ~0.64 us per
-  // split (the last block of a tile adds every partial).  Large tiles (one block per CU):
+  // Small tiles (copier waves, two blocks per CU), in microseconds, fitted to MI355X timings
+  // of the decoder's four GEMM shapes at 8, 99, 163 and 235 rows: ~0.95 us per split (the
+  // last block of a tile adds every partial), and per K group of a block ~0.42 us while the
+  // blocks fit one per CU, rising with the blocks per CU.  Large tiles (one block per CU):
   // rounds x (groups + fill) in group units plus a reduction term.
   int bestS = 1;
   double best = 1e30;
@@ -552,9 +552,8 @@ Plan make_plan(const GemmArgs &a, int bits, int ptype) {
     if (large) {
       cost = rounds * (gps + 3) + (S > 1 ? 2 : 0);
     } else {
-      const double per_cu = (double)std::min(blocks, slots) / std::max(1, a.n_cu);
-      cost = 0.674 * rounds * gps - 0.091 * rounds * gps * std::max(0.0, per_cu - 1.0) +
-             (S > 1 ? 3.2 : 0.0) + 0.636 * S + 6.65 * (rounds - 1);
+      const double per_cu = (double)blocks / std::max(1, a.n_cu);
+      cost = 0.953 * S - 1.044 * gps * rounds + 1.462 * gps * std::max(1.0, per_cu);
     }
     if (cost < best) {
       best = cost;
