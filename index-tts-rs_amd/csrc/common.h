@@ -189,7 +189,7 @@ __device__ inline float gelu_tanh(float x) {
 // same order on every block (deterministic).
 template <int NT>
 __device__ inline float block_sum(float v, float *red) {
-  v = wave_sum(v);
+  v = wave64_sum_dpp(v);
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();

@@ -570,7 +570,7 @@ __device__ inline void put_split(const SplitOut &o, size_t i, size_t gi, float v
   split_f16(v, h, l);
   o.hi[i] = (uint16_t)h;
   o.lo[i] = (uint16_t)l;
-  const float s = wave_sum(v);
+  const float s = wave64_sum_dpp(v);
   if ((threadIdx.x & 63) == 0) o.gs[gi] = s;
 }
 
