@@ -24,7 +24,7 @@ __device__ inline float rope_inv(int k) { return 1.0f / powf(10000.0f, (float)(2
 
 // Block sum over 256 threads; red holds 8 floats.
 __device__ inline float block_sum256(float v, float *red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = wave64_sum_dpp(v);
   const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[w] = v;

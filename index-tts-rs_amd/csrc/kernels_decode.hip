@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
         acc += pr[r][j].x * d + pr[r][j].y * xsum[c];
       }
     }
-    acc = wave_sum(acc);
+    acc = wave64_sum_dpp(acc);
     if (lane == 0 && row < N) {
       const float v = acc + a.ql.bias[row];
       if constexpr (EPI == kEpiStore) {
@@ -371,9 +371,9 @@ __device__ inline void attn_decode_block(const float *q, const void *kc, const v
     }
     sc = dot * 0.125f;
   }
-  const float mw = wave_max(sc);
+  const float mw = wave64_max_dpp(sc);
   const float p = (j < L) ? __expf(sc - mw) : 0.0f;
-  const float lw = wave_sum(p);
+  const float lw = wave64_sum_dpp(p);
   sh.p[wave][lane] = p;
   __syncthreads();
   float o8[8];
@@ -385,10 +385,13 @@ __device__ inline void attn_decode_block(const float *q, const void *kc, const v
 #pragma unroll
     for (int e = 0; e < 8; e++) o8[e] += pk * v8[kk][e];
   }
+  // add the key groups (lanes dg, dg + 8, .., dg + 56): lane ^ 8 by DPP (row_ror:8), lane ^ 16
+  // by swizzle, lane ^ 32 by one permute
 #pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) o8[e] += __shfl_xor(o8[e], off, 64);
+  for (int e = 0; e < 8; e++) {
+    o8[e] += dpp_pair<0x128>(o8[e]);
+    o8[e] += swizzle_xor16(o8[e]);
+    o8[e] += __shfl_xor(o8[e], 32, 64);
   }
   if (kg == 0) {
 #pragma unroll
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(64) void attn_combine_batch_kernel(const float *par
   const size_t i = (size_t)b * d + h * 64 + lane;
   out.hi[i] = (uint16_t)hi;
   out.lo[i] = (uint16_t)lo;
-  const float gsum = wave_sum(v);
+  const float gsum = wave64_sum_dpp(v);
   if (lane == 0) out.gs[(size_t)b * (d / 64) + h] = gsum;
 }
 
@@ -551,8 +554,8 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
   // element lane % 8 of lane lane / 8
 #pragma unroll
   for (int e = 0; e < 8; e++) {
-    acc[e] += __shfl_xor(acc[e], 8, 64);
-    acc[e] += __shfl_xor(acc[e], 16, 64);
+    acc[e] += dpp_pair<0x128>(acc[e]);  // row_ror:8 = lane ^ 8
+    acc[e] += swizzle_xor16(acc[e]);
     acc[e] += __shfl_xor(acc[e], 32, 64);
   }
   o = 0.0f;
@@ -627,13 +630,13 @@ __global__ __launch_bounds__(256) void log_softmax_pick_kernel(const float *logi
   const float *x = logits + (size_t)blockIdx.x * V;
   float mx = -INFINITY;
   for (int i = threadIdx.x; i < V; i += 256) mx = fmaxf(mx, x[i]);
-  mx = wave_max(mx);
+  mx = wave64_max_dpp(mx);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   float s = 0.0f;
   for (int i = threadIdx.x; i < V; i += 256) s += expf(x[i] - mx);
-  s = wave_sum(s);
+  s = wave64_sum_dpp(s);
   if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
