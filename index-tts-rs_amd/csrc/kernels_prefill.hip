@@ -9,10 +9,11 @@
 // 4-bit codes enter as the fp16 values 16 + q (bit pattern 0x4C00 | q << 6), so the group
 // term uses b - 16 s in place of b.
 //
-// Block: 256 threads, 2 x 2 waves of (32 TM) x (32 TN) outputs, tile (64 TM) x (64 TN).
-// The K loop runs over 64-wide groups through an NS-stage ring of LDS buffers filled by
-// global->LDS DMA (no registers); each stage holds the hi/lo activation tile, the code
-// tile, the group sums and the (scale, bias) pairs.  Activation and code rows are XOR
+// Block: 512 threads, 2 x 2 worker waves of (32 TM) x (32 TN) outputs, tile (64 TM) x
+// (64 TN), and four copier waves.  The K loop runs over 64-wide groups through an NS-stage
+// ring of LDS buffers filled by global->LDS DMA (no registers) that only the copiers issue,
+// so the copies overlap the workers' MFMAs; each stage holds the hi/lo activation tile, the
+// code tile, the group sums and the (scale, bias) pairs.  Activation and code rows are XOR
 // swizzled in 16-byte chunks so that the MFMA fragment reads spread over the banks.
 // Small M is spread over the chip by splitting K: each split stores its partial tile,
 // and the last split to arrive at a tile (wrapping counter) adds the partials in split
