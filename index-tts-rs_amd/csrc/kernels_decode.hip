@@ -669,6 +669,68 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const EmbedRow *rows, c
   }
 }
 
+// One wave per row for d = 256 * NV (NV <= 8): lane l holds columns 256 j + 4 l .. + 3 of
+// pass j in registers (16-byte loads), the mean and variance are DPP wave sums (no LDS, no
+// barrier), and the 16 lanes of a DPP row hold one 64-column group, whose sum they form
+// with four DPP steps.  Same arithmetic as ln_rows_kernel (biased variance, eps 1e-5; with
+// w2, a second LayerNorm), summed in a different order.
+template <int NV>
+__device__ __forceinline__ void ln_regs(float4 (&v)[NV], const float *w, const float *b, int d, int lane) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = wave64_sum_dpp(s) / (float)d;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  const float rstd = 1.0f / sqrtf(wave64_sum_dpp(q) / (float)d + 1e-5f);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const float4 wj = reinterpret_cast<const float4 *>(w)[64 * j + lane];
+    const float4 bj = reinterpret_cast<const float4 *>(b)[64 * j + lane];
+    v[j].x = (v[j].x - mean) * rstd * wj.x + bj.x;
+    v[j].y = (v[j].y - mean) * rstd * wj.y + bj.y;
+    v[j].z = (v[j].z - mean) * rstd * wj.z + bj.z;
+    v[j].w = (v[j].w - mean) * rstd * wj.w + bj.w;
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void ln_rows_wave_kernel(const float *x, const float *w, const float *b,
+                                                           const float *w2, const float *b2, int T, int d,
+                                                           SplitOut y) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;  // whole waves leave together
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)row * d);
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) v[j] = xr[64 * j + lane];
+  ln_regs<NV>(v, w, b, d, lane);
+  if (w2) ln_regs<NV>(v, w2, b2, d, lane);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const size_t i = (size_t)row * d + 256 * j + 4 * lane;
+    uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+    split_f16(v[j].x, h0, l0);
+    split_f16(v[j].y, h1, l1);
+    split_f16(v[j].z, h2, l2);
+    split_f16(v[j].w, h3, l3);
+    *reinterpret_cast<uint2 *>(y.hi + i) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+    *reinterpret_cast<uint2 *>(y.lo + i) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+    // group 4 j + lane / 16: the 16 lanes of this DPP row
+    float g = (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    g += dpp_pair<0xB1>(g);
+    g += dpp_pair<0x4E>(g);
+    g += dpp_pair<0x141>(g);
+    g += dpp_pair<0x140>(g);
+    if ((lane & 15) == 0) y.gs[(size_t)row * (d / 64) + 4 * j + (lane >> 4)] = g;
+  }
+}
+
 // d is a multiple of 64, so each wave's 64 consecutive columns are one group.  With w2
 // set, a second LayerNorm follows (ln_f then final_norm before the head).
 __global__ __launch_bounds__(256) void ln_rows_kernel(const float *x, const float *w, const float *b,
@@ -754,7 +816,19 @@ hipError_t launch_embed_rows(const EmbedRow *rows, int T, const float *conds,
 hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T, int d,
                           const SplitOut &y, hipStream_t s, const float *w2, const float *b2) {
   if (d % 64 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, w2, b2, d, y);
+  const dim3 grid4((T + 3) / 4);
+  switch (d % 256 == 0 ? d / 256 : 0) {  // one wave per row when d = 256 * (1..8)
+    case 1: hipLaunchKernelGGL(ln_rows_wave_kernel<1>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 2: hipLaunchKernelGGL(ln_rows_wave_kernel<2>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 3: hipLaunchKernelGGL(ln_rows_wave_kernel<3>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 4: hipLaunchKernelGGL(ln_rows_wave_kernel<4>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 5: hipLaunchKernelGGL(ln_rows_wave_kernel<5>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 6: hipLaunchKernelGGL(ln_rows_wave_kernel<6>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 7: hipLaunchKernelGGL(ln_rows_wave_kernel<7>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    case 8: hipLaunchKernelGGL(ln_rows_wave_kernel<8>, grid4, dim3(256), 0, s, x, w, b, w2, b2, T, d, y); break;
+    default:
+      hipLaunchKernelGGL(ln_rows_kernel, dim3(T), dim3(256), sizeof(float) * (d + 8), s, x, w, b, w2, b2, d, y);
+  }
   return hipGetLastError();
 }
 
