@@ -330,8 +330,9 @@ struct AttnShared {
   float m[4], l[4];
 };
 
-// One block of the decode attention: head h, key split s of the n_splits splits.
-template <int KVT>
+// One block of the decode attention: head h, key split s of the n_splits splits.  With
+// WT, the partial is stored write-through (agent scope) for a combine in the same launch.
+template <int KVT, bool WT = false>
 __device__ inline void attn_decode_block(const float *q, const void *kc, const void *vc, int max_seq,
                                          const DecodeCtl *ctl, int static_len, float *part, int h, int s,
                                          int n_splits, AttnShared &sh) {
@@ -414,10 +415,21 @@ __device__ inline void attn_decode_block(const float *q, const void *kc, const v
       lsum += sh.l[w] * f;
       osum += sh.o[w][lane] * f;
     }
-    mine[2 + lane] = osum;
-    if (lane == 0) {
-      mine[0] = M;
-      mine[1] = lsum;
+    if constexpr (WT) {
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(mine) + 2 + lane, __float_as_uint(osum), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) {
+        __hip_atomic_store(reinterpret_cast<uint32_t *>(mine), __float_as_uint(M), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(reinterpret_cast<uint32_t *>(mine) + 1, __float_as_uint(lsum), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      mine[2 + lane] = osum;
+      if (lane == 0) {
+        mine[0] = M;
+        mine[1] = lsum;
+      }
     }
   }
 }
@@ -433,40 +445,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
 
 // Batched decode attention: grid (head, split, sequence); sequence b reads its query row
 // q[b], its cache (layer offset layer_off from its base) and its length from its control
-// block, and writes its partials at part + b * n_head * n_splits * 66.
+// block, and writes its partials at part + b * n_head * n_splits * 66 (write-through).  The
+// last split of a (sequence, head) to finish (wrapping device-scope counter cnt[b][h], zero
+// between launches) combines the partials in split order (global max, then the weighted
+// denominators and outputs) into the sequence's attention row in the GEMM's split form.
 template <int KVT>
 __global__ __launch_bounds__(256) void attn_decode_batch_kernel(const float *q, const BatchSeq *seqs, size_t layer_off,
-                                                                int max_seq, float *part) {
+                                                                int max_seq, float *part, uint32_t *cnt,
+                                                                SplitOut out) {
   const BatchSeq &sq = seqs[blockIdx.z];
   if (sq.ctl->done) return;
   __shared__ AttnShared sh;
-  const int H = gridDim.x, d = H * 64;
+  __shared__ uint32_t last;
+  const int H = gridDim.x, d = H * 64, h = blockIdx.x, s = blockIdx.y, b = blockIdx.z, NS = gridDim.y;
+  const int S = (sq.ctl->valid_len + 1 + kAttnKeys - 1) / kAttnKeys;  // active splits
+  if (s >= S) return;
   const size_t es = KVT == kKvBf16 ? 2 : 4;
   const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
   const void *vc = static_cast<const char *>(sq.v) + layer_off * es;
-  attn_decode_block<KVT>(q + (size_t)blockIdx.z * d, kc, vc, max_seq, sq.ctl, 0,
-                         part + (size_t)blockIdx.z * H * gridDim.y * 66, blockIdx.x, blockIdx.y, gridDim.y, sh);
-}
-
-// Combines the split partials of each (sequence, head) into the attention output row of
-// the sequence, in the GEMM's split form.  Finished sequences leave their row untouched.
-__global__ __launch_bounds__(64) void attn_combine_batch_kernel(const float *part, const BatchSeq *seqs, int n_splits,
-                                                                int d, SplitOut out) {
-  const int b = blockIdx.y, h = blockIdx.x, lane = threadIdx.x;
-  const DecodeCtl *ctl = seqs[b].ctl;
-  if (ctl->done) return;
-  const int H = gridDim.x;
-  const int S = (ctl->valid_len + 1 + kAttnKeys - 1) / kAttnKeys;
-  const float *ph = part + ((size_t)b * H + h) * n_splits * 66;
+  float *pb = part + (size_t)b * H * NS * 66;
+  attn_decode_block<KVT, true>(q + (size_t)b * d, kc, vc, max_seq, sq.ctl, 0, pb, h, s, NS, sh);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this block's partial is stored
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicInc(cnt + (size_t)b * H + h, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
+  __syncthreads();
+  if (!last || threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  const uint32_t *ph = reinterpret_cast<const uint32_t *>(pb + (size_t)h * NS * 66);
+  auto ld = [&](int i) {
+    return __uint_as_float(__hip_atomic_load(ph + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  };
   float M = -INFINITY;
-  for (int s = 0; s < S; s++) M = fmaxf(M, ph[s * 66]);
+  for (int s2 = 0; s2 < S; s2++) M = fmaxf(M, ld(s2 * 66));
   float den = 0.0f, num = 0.0f;
-  for (int s = 0; s < S; s++) {
-    const float m = ph[s * 66];
+  for (int s2 = 0; s2 < S; s2++) {
+    const float m = ld(s2 * 66);
     if (m == -INFINITY) continue;
     const float f = __expf(m - M);
-    den += ph[s * 66 + 1] * f;
-    num += ph[s * 66 + 2 + lane] * f;
+    den += ld(s2 * 66 + 1) * f;
+    num += ld(s2 * 66 + 2 + lane) * f;
   }
   const float v = num / den;
   uint32_t hi, lo;
@@ -764,17 +781,17 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
 int attn_decode_max_splits(int max_seq) { return (max_seq + kAttnKeys - 1) / kAttnKeys; }
 
 hipError_t launch_decode_batch_parts(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
-                                     int max_seq, float *part, const SplitOut &out, int kvt, hipStream_t s) {
+                                     int max_seq, float *part, uint32_t *cnt, const SplitOut &out, int kvt,
+                                     hipStream_t s) {
   const int S = attn_decode_max_splits(max_seq);
   dim3 grid(n_head, S, B);
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvBf16>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part);
+    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvBf16>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part,
+                       cnt, out);
   } else {
-    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvF32>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part);
+    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvF32>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part,
+                       cnt, out);
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_batch_kernel, dim3(n_head, B), dim3(64), 0, s, part, seqs, S, n_head * 64, out);
   return hipGetLastError();
 }
 
