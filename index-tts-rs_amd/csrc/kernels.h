@@ -161,7 +161,7 @@ hipError_t launch_split_rows(const float *x, int M, int K, const SplitOut &o, hi
 
 hipError_t launch_dequant(const DevQL &ql, int bits, int ptype, float *out, hipStream_t s);
 
-// Persistent decode step (kernels_persist.hip): one cooperative launch of B blocks
+// Persistent decode step (kernels_persist.hip): one launch of B blocks
 // (one per CU) runs a whole decode step.  Exchange words are (epoch << 32 | fp32 bits).
 constexpr int kCntStride = 32;  // one 128-byte line per head counter
 struct PersistArgs {

@@ -1,4 +1,4 @@
-// Persistent decode step for gfx950: one cooperative launch runs a whole decode step
+// Persistent decode step for gfx950: one launch of one block per CU runs a whole decode step
 // (embedding, every block, ln_f + final_norm + mel_head) on one block per CU.
 //
 // Why persistent.  A batch-1 step is a chain of ~120 dependent GEMV/attention phases over
@@ -953,10 +953,16 @@ size_t persist_lds_bytes(const PersistArgs &a) {
   return f * sizeof(float);
 }
 
+// A regular launch (a cooperative one costs ~17 us more per step on MI355X).  The blocks are
+// co-resident without the cooperative guarantee: the grid is one block per CU, the block's
+// LDS admits only one per CU (persist_fits), and the decoder's stream orders the launch after
+// every earlier kernel of the decoder.  Should another stream's work hold a CU anyway, the
+// resident blocks' polls time out (bounded waits) and the step returns an error instead of
+// waiting forever.
 hipError_t launch_decode_persist(PersistArgs a, int bits, int ptype, hipStream_t s) {
   void *args[] = {&a};
   const size_t lds = persist_lds_bytes(a);
-  return hipLaunchCooperativeKernel(persist_fn(bits, ptype), dim3(a.B), dim3(kThreads), args, (unsigned)lds, s);
+  return hipLaunchKernel(persist_fn(bits, ptype), dim3(a.B), dim3(kThreads), args, lds, s);
 }
 
 hipError_t persist_init() {

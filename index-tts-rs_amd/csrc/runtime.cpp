@@ -1294,7 +1294,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     return enqueue_decode_step(gpt, kv);
   };
   // capture one decode iteration (sample, then step) once per cache and parameters
-  // the persistent step is a cooperative launch: enqueued directly, never captured
+  // the persistent step is enqueued directly, never captured
   const bool use_graph = gpt->use_graph && !kv->persist;
   if (use_graph && (!kv->have_graph || !same_sampling(kv->gkey, ds))) {
     if (kv->gexec) {
