@@ -9,8 +9,8 @@
  *                                       generate_codes, generate_codes_after
  *   crates/core/src/config.rs           SamplingParams and its validated newtypes
  * The reference is a Rust API (no FFI; its core crate forbids `unsafe`,
- * crates/core/src/lib.rs:19), so a thin Rust crate binds these symbols; see
- * INTEGRATION.md for that binding.
+ * crates/core/src/lib.rs:19), so a thin Rust crate of `extern "C"` declarations and safe
+ * wrappers (HipGpt, HipCfm) binds these symbols.
  *
  * Conventions
  *  - Every fallible call returns itts_status; itts_last_error() gives the message of the
