@@ -1,5 +1,6 @@
-// sample_next_token (sampler.rs:191-284) as one 1024-thread block's device function, shared
-// by the standalone sampler kernel and the persistent decode step's in-kernel sampling.
+// sample_next_token (sampler.rs:191-284) as one 1024-thread block's device function, used by
+// the sampler kernel (one block per sequence: single decode, batched decode, and the
+// standalone itts_sample_next_token call).
 //
 // Bit-exactness.  Given the same fp32 logits, this returns the token the reference's
 // algorithm returns: every value-producing operation is the same IEEE operation in the
