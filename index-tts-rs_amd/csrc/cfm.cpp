@@ -106,7 +106,7 @@ struct itts_cfm {
   std::vector<WnLayer> wn;
   // per-forward workspace (sized for R = B*T rows)
   Buf emb, th, t1, t2, st, mods, wng, fmod, tdev;
-  Buf hA, hB, n, qkv, att, gu, act, xres, hpad, acts, rs, oacc, v, rope, apo, aml;
+  Buf hA, hB, n, qkv, att, gu, act, xres, hpad, acts, rs, oacc, v, rope, apo, aml, kvs;
   int rope_T = 0;  // sequence length the rope table holds
   std::vector<Buf> skips;
   // solve / API staging
@@ -158,6 +158,7 @@ itts_status ensure_rows(itts_cfm *m, int B, int T) {
   CK(m->oacc.ensure(R * d));
   CK(m->v.ensure(R * c.in_ch));
   for (auto &b : m->skips) CK(b.ensure(R * d));
+  CK(m->kvs.ensure(((size_t)cfm_kv_split_halves(B, T, c.n_heads) + 1) / 2));  // 16-bit values, float units
   const size_t S = (size_t)cfm_attn_splits(B, T, c.n_heads);
   if (S > 1) {
     CK(m->apo.ensure(S * R * d));
@@ -225,7 +226,8 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     const float *mod_a = m->mods.p + (size_t)(2 * i) * 2 * d, *mod_f = m->mods.p + (size_t)(2 * i + 1) * 2 * d;
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_a, na2, b.an_w, s));
     BL(gemm(bl, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
-    CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p, s));
+    CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p,
+                     reinterpret_cast<uint16_t *>(m->kvs.p), s));
     BL(gemm(bl, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
     BL(gemm(bl, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));

@@ -225,8 +225,11 @@ hipError_t cfm_rope_table(int T, float *tab, hipStream_t s);
 // Key splits the attention uses for this shape (1..8); with more than one, part_o holds
 // [S][B][T][d] and part_ml [S][B][H][T][2] floats.
 int cfm_attn_splits(int B, int T, int H);
+// kv_split: workspace of cfm_kv_split_halves(B, T, H) 16-bit values (K with rope and V as
+// fp16 hi/lo planes, built once per call and shared by every query tile).
+int cfm_kv_split_halves(int B, int T, int H);
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
-                         float *part_o, float *part_ml, hipStream_t s);
+                         float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);
 hipError_t cfm_gate(const float *acts, const float *in_b, const float *g, int ld_g, int R, int T, int d, float *act,
                     hipStream_t s);

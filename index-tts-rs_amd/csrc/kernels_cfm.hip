@@ -159,18 +159,72 @@ __device__ __forceinline__ void load8_rope(const float *p, const float2 *tab, in
 
 #define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
 
+// K (rope applied) and V of every (batch, head) as fp16 hi/lo planes, once per forward
+// instead of once per query tile: K planes [B][H][Tp][64], V planes transposed [B][H][64][Tp]
+// (keys contiguous), keys padded to Tp (a multiple of 64) with zeros.  ws holds the planes
+// kh, kl, vh, vl of B * H * Tp * 64 values each.  The values are the ones the attention
+// kernel formerly built while staging (same rope and split arithmetic).
+__global__ __launch_bounds__(256) void kv_split_kernel(const float *qkv, const float2 *tab, int B, int T, int Tp, int d,
+                                                       int H, uint16_t *ws) {
+  const size_t plane = (size_t)B * H * Tp * kHd;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long nk = (long)B * H * Tp * 8;  // K: one thread per (b, h, t, 8-dim chunk)
+  const size_t ld3 = 3 * (size_t)d;
+  if (i < nk) {
+    const int c = (int)(i & 7);
+    long r = i >> 3;
+    const int t = (int)(r % Tp);
+    r /= Tp;
+    const int h = (int)(r % H), b = (int)(r / H);
+    u32x4v hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+    if (t < T) {
+      float v[8];
+      load8_rope(qkv + ((size_t)b * T + t) * ld3 + d + h * kHd + c * 8, tab, t, c * 8, v);
+      split8(v, hi, lo);
+    }
+    const size_t o = (((size_t)b * H + h) * Tp + t) * kHd + c * 8;
+    *reinterpret_cast<u32x4v *>(ws + o) = hi;
+    *reinterpret_cast<u32x4v *>(ws + plane + o) = lo;
+    return;
+  }
+  // V: one thread per (b, h, 8-key chunk, dim), dim fastest (64 lanes read one row)
+  const long j = i - nk, nkc = Tp / 8;
+  if (j >= (long)B * H * nkc * kHd) return;
+  const int e = (int)(j & 63);
+  long r = j >> 6;
+  const int kc = (int)(r % nkc);
+  r /= nkc;
+  const int h = (int)(r % H), b = (int)(r / H);
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int t = kc * 8 + k;
+    v[k] = t < T ? qkv[((size_t)b * T + t) * ld3 + 2 * d + h * kHd + e] : 0.0f;
+  }
+  u32x4v hi, lo;
+  split8(v, hi, lo);
+  const size_t o = (((size_t)b * H + h) * kHd + e) * Tp + kc * 8;
+  *reinterpret_cast<u32x4v *>(ws + 2 * plane + o) = hi;
+  *reinterpret_cast<u32x4v *>(ws + 3 * plane + o) = lo;
+}
+
 // Keys are split over S blocks per query tile (blockIdx.z = b * S + split, kts key tiles
 // each) so that short sequences still fill the chip; with S > 1 each block writes its
 // unnormalised rows and their (max, denominator) to part_o [S][B][T][d] / part_ml
 // [S][B][H][T][2], combined by attn_combine_kernel.
-__global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const float2 *tab, int T, int d, int S,
-                                                       int kts, float *out, float *part_o, float *part_ml) {
+__global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const float2 *tab, const uint16_t *kvs,
+                                                       int Tp, int T, int d, int S, int kts, float *out,
+                                                       float *part_o, float *part_ml) {
   __shared__ AttnLds sh;
   const int h = blockIdx.x, q0 = blockIdx.y * kAq, b = blockIdx.z / S, sp = blockIdx.z % S;
   const int B = gridDim.z / S, H = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const size_t ld3 = 3 * (size_t)d;
   const float *base = qkv + (size_t)b * T * ld3;
+  // this (batch, head)'s planes from kv_split_kernel
+  const size_t plane = (size_t)B * H * Tp * kHd, bh = (size_t)b * H + h;
+  const uint16_t *kh_p = kvs + bh * Tp * kHd, *kl_p = kh_p + plane;
+  const uint16_t *vh_p = kvs + 2 * plane + bh * kHd * Tp, *vl_p = vh_p + plane;
 
   // Q fragments of this lane's row (operand layout: row lane & 31, dims kk*16 + (lane>>5)*8 ..)
   f16x8 qh[4], ql[4];
@@ -200,41 +254,28 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
   const int kend = min(T, (sp + 1) * kts * kAk);
   for (int kb = sp * kts * kAk; kb < kend; kb += kAk) {
     __syncthreads();  // the previous tile's operands are no longer read
-    {  // K rows (rotated): thread -> key tid/2, dims (tid&1)*32 .. +31
-      const int kr = tid >> 1, key = min(kb + kr, T - 1);
+    {  // K rows (rotated, split): thread -> key tid/2, 16-byte chunks (tid&1)*4 .. +3
+      const int kr = tid >> 1;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const int chunk = (tid & 1) * 4 + c;
-        float v[8];
-        load8_rope(base + (size_t)key * ld3 + d + h * kHd + chunk * 8, tab, key, chunk * 8, v);
-        u32x4v hi, lo;
-        split8(v, hi, lo);
+        const size_t o = (size_t)(kb + kr) * kHd + chunk * 8;
+        const u32x4v hi = *reinterpret_cast<const u32x4v *>(kh_p + o);
+        const u32x4v lo = *reinterpret_cast<const u32x4v *>(kl_p + o);
         *reinterpret_cast<u32x4v *>(&sh.k[0][swz(kr, chunk)]) = hi;
         *reinterpret_cast<u32x4v *>(&sh.k[1][swz(kr, chunk)]) = lo;
       }
     }
-    {  // V transposed: thread -> keys 2kp, 2kp+1, dims (tid&3)*16 .. +15
-      const int kp = tid >> 2;
-      const int k0 = min(kb + 2 * kp, T - 1), k1 = min(kb + 2 * kp + 1, T - 1);
+    {  // V transposed: thread -> (dim e, 8-key chunk ck) for four of the 512 (e, ck) pairs
 #pragma unroll
-      for (int c = 0; c < 2; c++) {
-        const int e0 = (tid & 3) * 16 + c * 8;
-        const float *va = base + (size_t)k0 * ld3 + 2 * d + h * kHd + e0;
-        const float *vb = base + (size_t)k1 * ld3 + 2 * d + h * kHd + e0;
-        const float4 a0 = *reinterpret_cast<const float4 *>(va), a1 = *reinterpret_cast<const float4 *>(va + 4);
-        const float4 b0 = *reinterpret_cast<const float4 *>(vb), b1 = *reinterpret_cast<const float4 *>(vb + 4);
-        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int e = e0 + j;
-          uint32_t ha, la, hb2, lb;
-          split_f16(a[j], ha, la);
-          split_f16(bb[j], hb2, lb);
-          const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
-          *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
-          *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
-        }
+      for (int c = 0; c < 4; c++) {
+        const int idx = tid * 4 + c, e = idx >> 3, ck = idx & 7;
+        const size_t o = (size_t)e * Tp + kb + ck * 8;
+        const u32x4v hi = *reinterpret_cast<const u32x4v *>(vh_p + o);
+        const u32x4v lo = *reinterpret_cast<const u32x4v *>(vl_p + o);
+        const int li = e * 64 + ((ck ^ ((e >> 1) & 7)) << 3);
+        *reinterpret_cast<u32x4v *>(&sh.vt[0][li]) = hi;
+        *reinterpret_cast<u32x4v *>(&sh.vt[1][li]) = lo;
       }
     }
     __syncthreads();
@@ -496,13 +537,19 @@ int cfm_attn_splits(int B, int T, int H) {
   const int kts = (tiles + S - 1) / S;
   return (tiles + kts - 1) / kts;  // no split without keys
 }
+int cfm_kv_split_halves(int B, int T, int H) { return B * H * ((T + kAk - 1) / kAk) * kAk * kHd * 4; }
+
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
-                         float *part_o, float *part_ml, hipStream_t s) {
-  if (d != H * kHd || T < 1) return hipErrorInvalidValue;
+                         float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s) {
+  if (d != H * kHd || T < 1 || !kv_split) return hipErrorInvalidValue;
   const int S = cfm_attn_splits(B, T, H), tiles = (T + kAk - 1) / kAk, kts = (tiles + S - 1) / S;
   if (S > 1 && (!part_o || !part_ml)) return hipErrorInvalidValue;
+  const int Tp = tiles * kAk;
+  const long nthreads = (long)B * H * Tp * 8 + (long)B * H * (Tp / 8) * kHd;
+  hipLaunchKernelGGL(kv_split_kernel, dim3(nblk(nthreads)), dim3(256), 0, s, qkv,
+                     reinterpret_cast<const float2 *>(rope_tab), B, T, Tp, d, H, kv_split);
   hipLaunchKernelGGL(cfm_attn_kernel, dim3(H, (T + kAq - 1) / kAq, B * S), dim3(128), 0, s, qkv,
-                     reinterpret_cast<const float2 *>(rope_tab), T, d, S, kts, out, part_o, part_ml);
+                     reinterpret_cast<const float2 *>(rope_tab), kv_split, Tp, T, d, S, kts, out, part_o, part_ml);
   if (S > 1)
     hipLaunchKernelGGL(attn_combine_kernel, dim3(nblk((long)B * T * d)), dim3(256), 0, s, part_o, part_ml, S, B, T, d,
                        out);
