@@ -65,9 +65,60 @@ __device__ __forceinline__ void split8(const float v[8], u32x4 &hi, u32x4 &lo) {
 
 #define MFMA16 __builtin_amdgcn_mfma_f32_32x32x16_f16
 
+// K and V of every head as fp16 hi/lo planes for keys 0..L-1, once per layer instead of
+// once per query tile: K planes [H][Lp][64], V planes transposed [H][64][Lp] (keys
+// contiguous), keys padded to Lp (a multiple of 64) with zeros.  ws holds kh, kl, vh, vl of
+// H * Lp * 64 values each; the values are the ones the flash kernel otherwise builds while
+// staging (same split).
 template <int KVT>
+__global__ __launch_bounds__(256) void kv_split_kernel(const void *kc, const void *vc, int ld, int H, int L, int Lp,
+                                                       uint16_t *ws) {
+  const size_t plane = (size_t)H * Lp * 64;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  const long nk = (long)H * Lp * 8;  // K: one thread per (h, key, 8-dim chunk)
+  if (i < nk) {
+    const int c = (int)(i & 7);
+    const long r = i >> 3;
+    const int t = (int)(r % Lp), h = (int)(r / Lp);
+    u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+    if (t < L) {
+      float v[8];
+      load8<KVT>(kc, ((size_t)h * ld + t) * 64 + c * 8, v);
+      split8(v, hi, lo);
+    }
+    const size_t o = ((size_t)h * Lp + t) * 64 + c * 8;
+    *reinterpret_cast<u32x4 *>(ws + o) = hi;
+    *reinterpret_cast<u32x4 *>(ws + plane + o) = lo;
+    return;
+  }
+  // V: one thread per (h, 8-key chunk, dim), dim fastest (64 lanes read one row)
+  const long j = i - nk, nkc = Lp / 8;
+  if (j >= (long)H * nkc * 64) return;
+  const int e = (int)(j & 63);
+  const long r = j >> 6;
+  const int kc8 = (int)(r % nkc), h = (int)(r / nkc);
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int t = kc8 * 8 + k;
+    const size_t idx = ((size_t)h * ld + min(t, L - 1)) * 64 + e;
+    const float x = KVT == kKvBf16 ? __uint_as_float((uint32_t) static_cast<const uint16_t *>(vc)[idx] << 16)
+                                   : static_cast<const float *>(vc)[idx];
+    v[k] = t < L ? x : 0.0f;
+  }
+  u32x4 hi, lo;
+  split8(v, hi, lo);
+  const size_t o = ((size_t)h * 64 + e) * Lp + kc8 * 8;
+  *reinterpret_cast<u32x4 *>(ws + 2 * plane + o) = hi;
+  *reinterpret_cast<u32x4 *>(ws + 3 * plane + o) = lo;
+}
+
+// PRE: K/V come from kv_split_kernel's planes (kvs, keys padded to Lp) and are staged by
+// 16-byte copies; otherwise they are read from the cache and split while staged.
+template <int KVT, bool PRE>
 __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, const void *kc, const void *vc,
-                                                         int ld, int base, int T, const int *kstart, SplitOut out) {
+                                                         int ld, int base, int T, const int *kstart, SplitOut out,
+                                                         const uint16_t *kvs, int Lp) {
   __shared__ FlashLds sh;
   const int h = blockIdx.x, q0 = blockIdx.y * kFQ;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -116,41 +167,70 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
   const int kmax = base + min(q0 + kFQ - 1, T - 1);
   for (int kb = (kmin / kFK) * kFK; kb <= kmax; kb += kFK) {
     __syncthreads();  // the previous tile's operands are no longer read
-    {  // K rows: thread -> key tid/2, dims (tid&1)*32 .. +31
-      const int kr = tid >> 1, key = min(kb + kr, ld - 1);
+    if constexpr (PRE) {
+      const size_t plane = (size_t)gridDim.x * Lp * 64;
+      {  // K rows: thread -> key tid/2, 16-byte chunks (tid&1)*4 .. +3
+        const int kr = tid >> 1;
+        const uint16_t *khp = kvs + ((size_t)h * Lp + kb + kr) * 64;
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const int chunk = (tid & 1) * 4 + c;
-        float v[8];
-        load8<KVT>(kh, (size_t)key * 64 + chunk * 8, v);
-        u32x4 hi, lo;
-        split8(v, hi, lo);
-        *reinterpret_cast<u32x4 *>(&sh.k[0][swz(kr, chunk)]) = hi;
-        *reinterpret_cast<u32x4 *>(&sh.k[1][swz(kr, chunk)]) = lo;
-      }
-    }
-    {  // V transposed: thread -> keys 2kp, 2kp+1, dims (tid&3)*16 .. +15
-      const int kp = tid >> 2;
-      const int k0 = min(kb + 2 * kp, ld - 1), k1 = min(kb + 2 * kp + 1, ld - 1);
-#pragma unroll
-      for (int c = 0; c < 2; c++) {
-        const int e0 = (tid & 3) * 16 + c * 8;
-        float a[8], b[8];
-        load8<KVT>(vh, (size_t)k0 * 64 + e0, a);
-        load8<KVT>(vh, (size_t)k1 * 64 + e0, b);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int e = e0 + j;
-          uint32_t ha, la, hb2, lb;
-          split_f16(a[j], ha, la);
-          split_f16(b[j], hb2, lb);
-          const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
-          *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
-          *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
+        for (int c = 0; c < 4; c++) {
+          const int chunk = (tid & 1) * 4 + c;
+          const u32x4 hi = *reinterpret_cast<const u32x4 *>(khp + chunk * 8);
+          const u32x4 lo = *reinterpret_cast<const u32x4 *>(khp + plane + chunk * 8);
+          *reinterpret_cast<u32x4 *>(&sh.k[0][swz(kr, chunk)]) = hi;
+          *reinterpret_cast<u32x4 *>(&sh.k[1][swz(kr, chunk)]) = lo;
         }
       }
+      {  // V transposed: thread -> (dim e, 8-key chunk ck) for four of the 512 pairs
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const int idx = tid * 4 + c, e = idx >> 3, ck = idx & 7;
+          const uint16_t *vp = kvs + 2 * plane + ((size_t)h * 64 + e) * Lp + kb + ck * 8;
+          const u32x4 hi = *reinterpret_cast<const u32x4 *>(vp);
+          const u32x4 lo = *reinterpret_cast<const u32x4 *>(vp + plane);
+          const int li = e * 64 + ((ck ^ ((e >> 1) & 7)) << 3);
+          *reinterpret_cast<u32x4 *>(&sh.vt[0][li]) = hi;
+          *reinterpret_cast<u32x4 *>(&sh.vt[1][li]) = lo;
+        }
+      }
+      __syncthreads();
+    } else {
+      {  // K rows: thread -> key tid/2, dims (tid&1)*32 .. +31
+        const int kr = tid >> 1, key = min(kb + kr, ld - 1);
+  #pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const int chunk = (tid & 1) * 4 + c;
+          float v[8];
+          load8<KVT>(kh, (size_t)key * 64 + chunk * 8, v);
+          u32x4 hi, lo;
+          split8(v, hi, lo);
+          *reinterpret_cast<u32x4 *>(&sh.k[0][swz(kr, chunk)]) = hi;
+          *reinterpret_cast<u32x4 *>(&sh.k[1][swz(kr, chunk)]) = lo;
+        }
+      }
+      {  // V transposed: thread -> keys 2kp, 2kp+1, dims (tid&3)*16 .. +15
+        const int kp = tid >> 2;
+        const int k0 = min(kb + 2 * kp, ld - 1), k1 = min(kb + 2 * kp + 1, ld - 1);
+  #pragma unroll
+        for (int c = 0; c < 2; c++) {
+          const int e0 = (tid & 3) * 16 + c * 8;
+          float a[8], b[8];
+          load8<KVT>(vh, (size_t)k0 * 64 + e0, a);
+          load8<KVT>(vh, (size_t)k1 * 64 + e0, b);
+  #pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const int e = e0 + j;
+            uint32_t ha, la, hb2, lb;
+            split_f16(a[j], ha, la);
+            split_f16(b[j], hb2, lb);
+            const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
+            *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
+            *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
+          }
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
 
     floatx16 S[2];
 #pragma unroll
@@ -246,15 +326,35 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
 
 }  // namespace
 
+size_t attn_kv_split_halves(int n_head, int keys) { return (size_t)n_head * ((keys + kFK - 1) / kFK) * kFK * 64 * 4; }
+
 hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart, const void *kc, const void *vc,
-                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s) {
+                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s, uint16_t *kv_split) {
   if (T <= 0 || base + T > ld) return hipErrorInvalidValue;
   dim3 grid(n_head, (T + kFQ - 1) / kFQ);
   const int d = n_head * 64;
+  if (kv_split) {
+    // keys 0 .. base + T - 1, padded to whole tiles
+    const int L = base + T, Lp = ((L + kFK - 1) / kFK) * kFK;
+    const long nthreads = (long)n_head * Lp * 8 + (long)n_head * (Lp / 8) * 64;
+    const dim3 sg((unsigned)((nthreads + 255) / 256));
+    if (kvt == kKvBf16) {
+      hipLaunchKernelGGL(kv_split_kernel<kKvBf16>, sg, dim3(256), 0, s, kc, vc, ld, n_head, L, Lp, kv_split);
+      hipLaunchKernelGGL((attn_flash_kernel<kKvBf16, true>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
+                         out, kv_split, Lp);
+    } else {
+      hipLaunchKernelGGL(kv_split_kernel<kKvF32>, sg, dim3(256), 0, s, kc, vc, ld, n_head, L, Lp, kv_split);
+      hipLaunchKernelGGL((attn_flash_kernel<kKvF32, true>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
+                         out, kv_split, Lp);
+    }
+    return hipGetLastError();
+  }
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_flash_kernel<kKvBf16>, grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart, out);
+    hipLaunchKernelGGL((attn_flash_kernel<kKvBf16, false>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
+                       out, nullptr, 0);
   } else {
-    hipLaunchKernelGGL(attn_flash_kernel<kKvF32>, grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart, out);
+    hipLaunchKernelGGL((attn_flash_kernel<kKvF32, false>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
+                       out, nullptr, 0);
   }
   return hipGetLastError();
 }

@@ -155,7 +155,7 @@ struct itts_gpt {
   DevBuf gws, gcnt;
   // replay / all-row forward: per-layer scratch K/V (fp32 [n_head][M][64]), key starts,
   // head logits, probe maps, codes and log-probabilities
-  DevBuf rk, rv, kstart, plog, pmap, pcodes, plp;
+  DevBuf rk, rv, kstart, plog, pmap, pcodes, plp, pkvs;
   int align_pairs[2][2] = {{4, 10}, {5, 10}};  // (layer, head), align/mod.rs:37
   int n_align = 2;
   // batched decode: residual rows, q rows, split-form rows, attention partials, logits,
@@ -523,6 +523,7 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
   const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
   HIP_TRY(g->rk.ensure(sizeof(float) * (size_t)M * d));
+  HIP_TRY(g->pkvs.ensure(sizeof(uint16_t) * attn_kv_split_halves(c.n_head, M)));
   HIP_TRY(g->rv.ensure(sizeof(float) * (size_t)M * d));
   HIP_TRY(g->kstart.ensure(sizeof(int) * (size_t)M));
   HIP_TRY(hipMemcpyAsync(g->kstart.p, kstart.data(), sizeof(int) * M, hipMemcpyHostToDevice, s));
@@ -537,7 +538,8 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
       if (p.layer == l)
         HIP_TRY(launch_attn_probe(Q, M, g->kstart.as<int>(), g->rk.p, g->rv.p, c.n_head,
                                   AttnProbe{p.head, p.q0, p.k0, p.k1, p.out}, kKvF32, s));
-    HIP_TRY(launch_attn_flash(Q, M, 0, g->kstart.as<int>(), g->rk.p, g->rv.p, M, c.n_head, g->pa.out(), kKvF32, s));
+    HIP_TRY(launch_attn_flash(Q, M, 0, g->kstart.as<int>(), g->rk.p, g->rv.p, M, c.n_head, g->pa.out(), kKvF32, s,
+                              g->pkvs.as<uint16_t>()));
     ga = gemm_args(g, L.proj, g->pa.act(), M);
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
