@@ -78,6 +78,36 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float *x, float *y, in
   for (int i = threadIdx.x; i < d; i += 256) y[(size_t)r * d + i] = w[i] * (xr[i] * rs * norm_w[i]) + bb[i];
 }
 
+// adaln_kernel with one wave per row for d = 256 * NV: lane l holds columns 256 j + 4 l ..
+// + 3 of pass j in registers, the mean square is a DPP wave sum (no LDS, no barrier).
+template <int NV>
+__global__ __launch_bounds__(256) void adaln_wave_kernel(const float *x, float *y, int R, int T, int d,
+                                                         const float *mod, int ld_mod, const float *norm_w) {
+  const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;  // whole waves leave together
+  const int b = r / T;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)r * d);
+  float4 v[NV];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    v[j] = xr[64 * j + lane];
+    s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  }
+  const float rs = 1.0f / sqrtf(wave64_sum_dpp(s) / (float)d + 1e-5f);
+  const float4 *w = reinterpret_cast<const float4 *>(mod + (size_t)b * ld_mod);
+  const float4 *bb = reinterpret_cast<const float4 *>(mod + (size_t)b * ld_mod + d);
+  const float4 *nw = reinterpret_cast<const float4 *>(norm_w);
+  float4 *yr = reinterpret_cast<float4 *>(y + (size_t)r * d);
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int c = 64 * j + lane;
+    const float4 wj = w[c], bj = bb[c], nj = nw[c];
+    yr[c] = make_float4(wj.x * (v[j].x * rs * nj.x) + bj.x, wj.y * (v[j].y * rs * nj.y) + bj.y,
+                        wj.z * (v[j].z * rs * nj.z) + bj.z, wj.w * (v[j].w * rs * nj.w) + bj.w);
+  }
+}
+
 // FinalLayer norm (cfm.rs:605-609): layer_norm(h, eps 1e-6, no affine) * (1 + scale_b) +
 // shift_b, (shift_b, scale_b) = mod[b][0..d), mod[b][d..2d).
 __global__ __launch_bounds__(256) void final_norm_kernel(const float *x, float *y, int T, int d, const float *mod) {
@@ -517,7 +547,14 @@ hipError_t cfm_add_bias(float *C, int ldc, const float *bias, int rows, int cols
 }
 hipError_t cfm_adaln(const float *x, float *y, int R, int T, int d, const float *mod, int ld_mod, const float *norm_w,
                      hipStream_t s) {
-  hipLaunchKernelGGL(adaln_kernel, dim3(R), dim3(256), 0, s, x, y, T, d, mod, ld_mod, norm_w);
+  // one wave per row when d = 256 or 512 and the modulation rows keep 16-byte alignment
+  const bool wave = (d == 256 || d == 512) && ld_mod % 4 == 0;
+  if (wave && d == 512)
+    hipLaunchKernelGGL(adaln_wave_kernel<2>, dim3((R + 3) / 4), dim3(256), 0, s, x, y, R, T, d, mod, ld_mod, norm_w);
+  else if (wave)
+    hipLaunchKernelGGL(adaln_wave_kernel<1>, dim3((R + 3) / 4), dim3(256), 0, s, x, y, R, T, d, mod, ld_mod, norm_w);
+  else
+    hipLaunchKernelGGL(adaln_kernel, dim3(R), dim3(256), 0, s, x, y, T, d, mod, ld_mod, norm_w);
   return hipGetLastError();
 }
 hipError_t cfm_final_norm(const float *x, float *y, int R, int T, int d, const float *mod, hipStream_t s) {
