@@ -3,15 +3,17 @@
 //
 // CfmDit::from_weights -> itts_cfm_create (tensors by checkpoint name, checked by element
 // count), forward_merged -> itts_cfm_forward, solve_euler -> itts_cfm_solve_euler.  The
-// estimator runs in fp32: its linears (and WaveNet's kernel-5 convolution, as five shifted
-// GEMMs over a zero-padded buffer) are rocBLAS sgemm calls on the estimator's stream; the
-// kernels in kernels_cfm.hip do the rest.  Layout: activations [B][T][C] row-major, the CFG
+// estimator keeps fp32 activations: its linears (and WaveNet's kernel-5 convolution, as one
+// GEMM over a zero-padded buffer whose operand rows overlap) run on the split-fp16 MFMA GEMM
+// of kernels_cfm.hip on the estimator's stream, products under 64 rows on rocBLAS sgemm;
+// the other kernels in kernels_cfm.hip do the rest.  Layout: activations [B][T][C] row-major, the CFG
 // pair as batch rows 0 (conditioned) and 1 (unconditioned).
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -75,10 +77,26 @@ struct Buf {
   }
 };
 
-// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart): the column-major
-// product y^T = W A^T.
+// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart).  Row blocks of 64 and
+// more run on the split-fp16 MFMA GEMM on the handle's stream; smaller ones (the per-batch
+// timestep and style projections) and operands it cannot take go to rocBLAS as the
+// column-major product y^T = W A^T.  ITTS_CFM_ROCBLAS=1 sends every product to rocBLAS.
+bool force_rocblas() {
+  static const bool f = [] {
+    const char *e = std::getenv("ITTS_CFM_ROCBLAS");
+    return e && e[0] == '1';
+  }();
+  return f;
+}
 rocblas_status gemm(rocblas_handle h, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
                     int ldy, float beta) {
+  if (M >= 64 && !force_rocblas() && itts::cfm_gemm_fits(A, lda, W, ldw, K)) {
+    hipStream_t st = nullptr;
+    if (rocblas_get_stream(h, &st) != rocblas_status_success) return rocblas_status_internal_error;
+    return itts::cfm_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st) == hipSuccess
+               ? rocblas_status_success
+               : rocblas_status_internal_error;
+  }
   const float one = 1.0f;
   return rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W, ldw, A, lda, &beta, y,
                        ldy);
@@ -251,11 +269,17 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     const bool last = l + 1 == NL;
     const int rso = last ? d : 2 * d;
     const float one = 1.0f;
-    for (int k = 0; k < K; k++) {  // tap k reads padded rows t + k
-      const float beta = k == 0 ? 0.0f : 1.0f;
-      BL(rocblas_sgemm_strided_batched(bl, rocblas_operation_transpose, rocblas_operation_none, 2 * d, T, d, &one,
-                                       w.in_w + (size_t)k * d, K * d, 0, m->hpad.p + (size_t)k * d, d, sp, &beta,
-                                       m->acts.p, 2 * d, (long)T * 2 * d, B));
+    if (!force_rocblas() && cfm_gemm_fits(m->hpad.p, d, w.in_w, K * d, K * d)) {
+      // all taps as one product: row t of the padded input read K * d wide (rows t .. t+K-1)
+      CK(cfm_gemm(B, T, 2 * d, K * d, m->hpad.p, d, sp, w.in_w, K * d, 0, m->acts.p, 2 * d, (long)T * 2 * d, 0.0f,
+                  s));
+    } else {
+      for (int k = 0; k < K; k++) {  // tap k reads padded rows t + k
+        const float beta = k == 0 ? 0.0f : 1.0f;
+        BL(rocblas_sgemm_strided_batched(bl, rocblas_operation_transpose, rocblas_operation_none, 2 * d, T, d, &one,
+                                         w.in_w + (size_t)k * d, K * d, 0, m->hpad.p + (size_t)k * d, d, sp, &beta,
+                                         m->acts.p, 2 * d, (long)T * 2 * d, B));
+      }
     }
     CK(cfm_gate(m->acts.p, w.in_b, m->wng.p + (size_t)l * 2 * d, 2 * d * NL, R, T, d, m->act.p, s));
     BL(gemm(bl, R, rso, d, m->act.p, d, w.rs_w, d, m->rs.p, rso, 0.0f));

@@ -232,6 +232,13 @@ int cfm_attn_splits(int B, int T, int H);
 // kv_split: workspace of cfm_kv_split_halves(B, T, H) 16-bit values (K with rope and V as
 // fp16 hi/lo planes, built once per call and shared by every query tile).
 int cfm_kv_split_halves(int B, int T, int H);
+// y[z] = A[z] W[z]^T + beta y[z] for z < batch (row-major; A rows lda apart and allowed to
+// overlap, W rows ldw apart, batch strides sa / sw / sy in floats) on the MFMA units with fp16
+// hi/lo operands and fp32 accumulation.  cfm_gemm_fits: K, lda, ldw multiples of 4 and A, W
+// 16-byte aligned (the launch rejects anything else).
+bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K);
+hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
+                    float *y, int ldy, long sy, float beta, hipStream_t s);
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
                          float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);

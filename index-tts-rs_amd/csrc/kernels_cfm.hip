@@ -423,6 +423,114 @@ __global__ void attn_combine_kernel(const float *part_o, const float *part_ml, i
   out[i] = num / den;
 }
 
+// y[z][M][N] = A[z][M][K] W[z][N][K]^T + beta y on the MFMA units (the estimator's fp32
+// Linear and conv layers, cfm.rs:200-411).  Operands are split into fp16 hi/lo planes as
+// they are staged, y = Ah Wh + Ah Wl + Al Wh with fp32 accumulation (~22-bit operands, as
+// in the attention above).  Block: 8 waves, a 64 x 64 tile of y; waves w and w + 4 share
+// the 32 x 32 quarter w on v_mfma_f32_32x32x16_f16, each taking half of every K tile (two
+// waves per SIMD even when the tiles only cover the chip once), their sums added through
+// LDS at the end in a fixed order.  K in tiles of 64, double-buffered in LDS ([plane][row][k]
+// with 16-byte chunks XOR-swizzled by row), the next tile's fp32 loads in flight while the
+// MFMA units work on the current one: one barrier per K tile.  Rows of A may overlap (lda < K):
+// a kernel-size-k conv over rows d apart is one GEMM with K = k d and lda = d.
+// Requires K, lda, ldw % 4 == 0 and 16-byte aligned A and W.
+// (a, b) -> packed fp16 pairs hi = (ha, hb), lo = (la, lb) with a = ha + la, b = hb + lb
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  uint32_t h0, l0, h1, l1;
+  split_f16(a, h0, l0);
+  split_f16(b, h1, l1);
+  hi = h0 | (h1 << 16);
+  lo = l0 | (l1 << 16);
+}
+
+struct GemmLds {
+  uint16_t a[2][2][64 * 64];  // [buffer][plane][row][k]
+  uint16_t w[2][2][64 * 64];
+};
+
+__global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const float *W, int ldw,
+                                                         long sw, float *y, int ldy, long sy, int M, int N, int K,
+                                                         float beta) {
+  __shared__ GemmLds sh;
+  const int tid = threadIdx.x, lane = tid & 63, wv = (tid >> 6) & 3, kg = tid >> 8, wm = wv >> 1, wn = wv & 1;
+  const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
+  A += blockIdx.z * sa;
+  W += blockIdx.z * sw;
+  y += blockIdx.z * sy;
+  const int nk = (K + 63) / 64;
+  float4 ra[2], rw[2];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int idx = tid + 512 * j, row = idx >> 4, k = kt * 64 + (idx & 15) * 4;
+      ra[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      rw[j] = ra[j];
+      if (m0 + row < M && k < K) ra[j] = *reinterpret_cast<const float4 *>(A + (size_t)(m0 + row) * lda + k);
+      if (n0 + row < N && k < K) rw[j] = *reinterpret_cast<const float4 *>(W + (size_t)(n0 + row) * ldw + k);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int idx = tid + 512 * j, row = idx >> 4, c4 = idx & 15;
+      const int off = swz(row, c4 >> 1) + (c4 & 1) * 4;
+      uint32_t ah0, al0, ah1, al1, wh0, wl0, wh1, wl1;
+      split2(ra[j].x, ra[j].y, ah0, al0);
+      split2(ra[j].z, ra[j].w, ah1, al1);
+      split2(rw[j].x, rw[j].y, wh0, wl0);
+      split2(rw[j].z, rw[j].w, wh1, wl1);
+      *reinterpret_cast<uint2 *>(&sh.a[buf][0][off]) = make_uint2(ah0, ah1);
+      *reinterpret_cast<uint2 *>(&sh.a[buf][1][off]) = make_uint2(al0, al1);
+      *reinterpret_cast<uint2 *>(&sh.w[buf][0][off]) = make_uint2(wh0, wh1);
+      *reinterpret_cast<uint2 *>(&sh.w[buf][1][off]) = make_uint2(wl0, wl1);
+    }
+  };
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt++) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load(kt + 1);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++) {
+      const int kk = kg * 2 + k2;
+      const int oa = swz(wm * 32 + (lane & 31), kk * 2 + (lane >> 5));
+      const int ob = swz(wn * 32 + (lane & 31), kk * 2 + (lane >> 5));
+      const f16x8 ah = *reinterpret_cast<const f16x8 *>(&sh.a[buf][0][oa]);
+      const f16x8 al = *reinterpret_cast<const f16x8 *>(&sh.a[buf][1][oa]);
+      const f16x8 bh = *reinterpret_cast<const f16x8 *>(&sh.w[buf][0][ob]);
+      const f16x8 bl = *reinterpret_cast<const f16x8 *>(&sh.w[buf][1][ob]);
+      acc = MFMA16(ah, bh, acc, 0, 0, 0);
+      acc = MFMA16(ah, bl, acc, 0, 0, 0);
+      acc = MFMA16(al, bh, acc, 0, 0, 0);
+    }
+    if (kt + 1 < nk) store(buf ^ 1);
+    __syncthreads();
+  }
+  // the second K half's sums to LDS (the loop ended on a barrier), added by the first
+  float *red = reinterpret_cast<float *>(&sh.a[0][0][0]) + wv * 1024 + lane;
+  if (kg == 1) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) red[i * 64] = acc[i];
+  }
+  __syncthreads();
+  const int c = n0 + wn * 32 + (lane & 31);
+  if (kg == 1 || c >= N) return;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] += red[i * 64];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = m0 + wm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+    if (r < M) {
+      float *o = y + (size_t)r * ldy + c;
+      *o = beta == 0.0f ? acc[i] : acc[i] + beta * *o;
+    }
+  }
+}
+
 // SwiGLU (cfm.rs:306-311): out[r][i] = silu(gu[r][i]) * gu[r][F + i]
 __global__ void swiglu_kernel(const float *gu, int R, int F, float *out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -590,6 +698,17 @@ hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, 
   if (S > 1)
     hipLaunchKernelGGL(attn_combine_kernel, dim3(nblk((long)B * T * d)), dim3(256), 0, s, part_o, part_ml, S, B, T, d,
                        out);
+  return hipGetLastError();
+}
+bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K) {
+  return K % 4 == 0 && lda % 4 == 0 && ldw % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(W) & 15) == 0;
+}
+hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
+                    float *y, int ldy, long sy, float beta, hipStream_t s) {
+  if (batch < 1 || M < 1 || N < 1 || K < 1 || !cfm_gemm_fits(A, lda, W, ldw, K)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(split_gemm_kernel, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa, W,
+                     ldw, sw, y, ldy, sy, M, N, K, beta);
   return hipGetLastError();
 }
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s) {
