@@ -247,9 +247,9 @@ def cfm_solve(seed):
             "solve_ms": round(dev, 2), "host_call_ms": round(statistics.median(walls), 2),
             "reference_ms": 1540.0, "speedup_vs_reference": round(1540.0 / dev, 2),
             "tflop_per_solve": round(tflop, 3), "achieved_tflops": round(tflop / (dev * 1e-3), 1),
-            "peak_tflops": 157.3, "frac": round(tflop / (dev * 1e-3) / 157.3, 4),
-            "note": "fp32: linears and WaveNet convolutions in rocBLAS sgemm, attention and elementwise in HIP "
-                    "kernels; peak = fp32 MFMA dense"}
+            "peak_tflops": 833.3, "frac": round(tflop / (dev * 1e-3) / 833.3, 4),
+            "note": "fp32 activations; linears, WaveNet convolutions and attention on fp16 hi/lo split MFMA "
+                    "(three fp16 products per product, fp32 accumulation); peak = fp16 dense 2.5 PFLOP/s / 3"}
 
 
 def main():

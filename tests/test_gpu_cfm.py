@@ -1,8 +1,9 @@
 """CFM DiT estimator and Euler / CFG solver on the HIP path, through the C ABI, against the
 oracle's restatement of cfm.rs (forward_merged 545-617, solve_euler 619-760).
 
-Both sides compute in fp32 with different summation orders (rocBLAS sgemm vs the oracle's
-double accumulation), so the bar is relative: max |gpu - oracle| / max |oracle| below 2e-4
+The HIP path keeps fp32 activations and contracts on fp16 hi/lo split MFMA products (~22-bit
+operands, fp32 accumulation, its own summation order) against the oracle's double
+accumulation, so the bar is relative: max |gpu - oracle| / max |oracle| below 2e-4
 for one forward and 1e-3 after several Euler steps."""
 import sys
 
