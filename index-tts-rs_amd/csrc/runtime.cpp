@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -23,6 +24,7 @@ using namespace itts;
 namespace {
 
 thread_local std::string g_last_error;
+constexpr int kMaxDevices = 64;  // device ordinals the library accepts
 
 itts_status set_error(itts_status st, const char *fmt, ...) {
   char buf[512];
@@ -144,6 +146,7 @@ struct itts_gpt {
   // persistent decode step: device copy of `layers`, blocks (one per compute unit)
   DevBuf dlayers;
   int n_cu = 0;
+  int device = 0;
   bool persist_ok = false;  // kernels set up (int8 or int4 codes)
   itts_decode_path path = ITTS_DECODE_AUTO;
   // decode workspace
@@ -397,11 +400,34 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
 
 // Enqueues one decode step driven by kv->ctl (token, position and cache length read on
 // the device): logits land in gpt->logits and ctl->valid_len advances.
+// Persistent decode steps of different decoders must not run at the same time.  A step's
+// blocks wait for each other's exchange words and assume that together they hold every
+// compute unit; two steps dispatched together from two streams could each get part of the
+// chip and wait for blocks that cannot start before the other step ends (the bounded waits
+// would then fail both).  Persistent launches are therefore chained per device: a launch on
+// a stream other than the previous launch's first waits for that launch's completion
+// event, and every launch records the event.  Steps of one decoder share its stream and
+// are ordered by it already.
+struct PersistChain {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+};
+PersistChain g_persist_chain[kMaxDevices];
+
+itts_status launch_persist_chained(itts_gpt *g, itts_kv *kv) {
+  PersistChain &ch = g_persist_chain[g->device];
+  std::lock_guard<std::mutex> lock(ch.mu);
+  if (!ch.done) HIP_TRY(hipEventCreateWithFlags(&ch.done, hipEventDisableTiming));
+  if (ch.last && ch.last != g->stream) HIP_TRY(hipStreamWaitEvent(g->stream, ch.done, 0));
+  HIP_TRY(launch_decode_persist(kv->pa, g->cfg.quant_bits, g->ptype(), g->stream));
+  HIP_TRY(hipEventRecord(ch.done, g->stream));
+  ch.last = g->stream;
+  return ITTS_OK;
+}
+
 itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
-  if (kv->persist) {
-    HIP_TRY(launch_decode_persist(kv->pa, g->cfg.quant_bits, g->ptype(), g->stream));
-    return ITTS_OK;
-  }
+  if (kv->persist) return launch_persist_chained(g, kv);
   const itts_config &c = g->cfg;
   const int d = c.d_model, bits = c.quant_bits, pt = g->ptype();
   hipStream_t s = g->stream;
@@ -922,10 +948,11 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
     return fail(set_error(ITTS_E_DEVICE, "upload of the layer table failed"));
   {
     int dev = 0, coop = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices ||
         hipDeviceGetAttribute(&g->n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
+    g->device = dev;
     g->persist_ok = (bits == 8 || bits == 4) && coop != 0 && persist_init() == hipSuccess;
   }
   if (g->gws.ensure(sizeof(float) * gemm_ws_floats(g->n_cu)) || g->gcnt.ensure(sizeof(uint32_t) * kGemmCounters) ||
@@ -942,6 +969,13 @@ static void gpt_release(itts_gpt *gpt) {
   if (--gpt->refs > 0) return;
   if (gpt->stream) {
     (void)hipStreamSynchronize(gpt->stream);
+    {
+      // a later decoder's stream may reuse this handle value: forget it as the last
+      // persistent launcher (its work has drained)
+      PersistChain &ch = g_persist_chain[gpt->device];
+      std::lock_guard<std::mutex> lock(ch.mu);
+      if (ch.last == gpt->stream) ch.last = nullptr;
+    }
     (void)hipStreamDestroy(gpt->stream);
   }
   delete gpt;

@@ -27,3 +27,32 @@ def tiny_prompt(tiny_weights):
     from itts_hip import synth
 
     return synth.make_prompt(tiny_weights.cfg, n_cond=3, n_text=12, seed=5)
+
+
+def _full(cfg_over, seed):
+    import ito
+    import itts_hip as H
+    from itts_hip import synth
+
+    print(f"[gpu] full-size decoder weights {cfg_over or ''} seed {seed}", flush=True)
+    W = synth.make_weights(dict(synth.FULL_CONFIG, **cfg_over), seed=seed)
+    ito.lib.ito_set_threads(16)
+    g = H.Gpt(W)
+    return W, g, ito.Model(W)
+
+
+@pytest.fixture(scope="session")
+def full_model():
+    """The decoder at its real shape (int8 codes, fp16 group params, spec init): weights,
+    the HIP decoder and the oracle over the same arrays."""
+    W, g, M = _full({}, 11)
+    yield W, g, M
+    g.close()
+
+
+@pytest.fixture(scope="session")
+def full_int4():
+    """The real shape with 4-bit codes."""
+    W, g, M = _full({"quant_bits": 4}, 13)
+    yield W, g, M
+    g.close()

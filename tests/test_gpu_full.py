@@ -26,13 +26,8 @@ def say(*a):
 
 
 @pytest.fixture(scope="module")
-def full():
-    say("[gpu] full-size decoder: weights")
-    W = synth.make_weights(synth.FULL_CONFIG, seed=11)
-    g = H.Gpt(W)
-    ito.lib.ito_set_threads(16)
-    yield W, g, ito.Model(W)
-    g.close()
+def full(full_model):
+    return full_model
 
 
 @pytest.mark.parametrize("n_cond,n_text", [(32, 64), (32, 200), (32, 500)])
@@ -207,13 +202,11 @@ def test_full_generate_batch(full):
 
 
 @pytest.mark.parametrize("path", [H.ITTS_DECODE_AUTO, H.ITTS_DECODE_MULTI])
-def test_full_int4_steps(path):
+def test_full_int4_steps(full_int4, path):
     """4-bit weights at the real shape (persistent step by default, or the multi-kernel
     step): prefill of 32 + 128 text ids and 16 teacher-forced steps against the oracle."""
     say(f"[gpu] full int4 decoder, path {path}")
-    W = synth.make_weights(dict(synth.FULL_CONFIG, quant_bits=4), seed=13)
-    g = H.Gpt(W)
-    M = ito.Model(W)
+    W, g, M = full_int4
     try:
         g.set_decode_path(path)
         pr = synth.make_prompt(W.cfg, 32, 128, seed=3)
@@ -227,4 +220,4 @@ def test_full_int4_steps(path):
         say(f"[gpu]   worst max |logit diff| {worst:.3g}")
         assert worst < LOGIT_TOL and worst < 2e-3
     finally:
-        g.close()
+        g.set_decode_path(H.ITTS_DECODE_AUTO)
