@@ -233,6 +233,16 @@ void itts_seen_insert(uint64_t words[129], int32_t token_id);
 itts_status itts_sample_next_token(itts_gpt *gpt, float *logits, int32_t n,
                                    const uint64_t seen[129], const itts_sampling *p,
                                    uint64_t *rng_state, int32_t *token_out);
+/* itts_sample_next_token without any device allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, results and errors, but the logits, seen words and
+ * RNG state are staged in a static device array of the library (one per device, about
+ * 37 KB, held until the process ends) instead of buffers it allocates; n is limited to
+ * 9216.  Calls on one device share that array: the library serialises its own calls,
+ * and two processes have separate arrays. */
+itts_status itts_sample_next_token_noalloc(itts_gpt *gpt, float *logits, int32_t n,
+                                           const uint64_t seen[129], const itts_sampling *p,
+                                           uint64_t *rng_state, int32_t *token_out);
 
 /* generate_codes_after (sampler.rs:340-392) with the whole loop on the device: prefill,
  * then per step STOP masking (min_codes), repetition penalty, sampling and the next

@@ -216,6 +216,24 @@ hipError_t launch_sampler(float *logits, int n, const uint64_t *seen, DevSamplin
 hipError_t launch_sampler_batch(float *logits, int n, const DevSampling *ps, const BatchSeq *seqs, int B,
                                 int stop_tok, int lds_top_k, bool any_sampled, hipStream_t s);
 
+// Device ordinals the library accepts.
+constexpr int kMaxDevices = 64;
+// Staging area of the sampler's no-allocation entry point: a static device array (one per
+// device, held until the process ends) with room for kStageMaxLogits logits, the seen-set
+// words, the RNG state and the token.
+constexpr int kStageMaxLogits = 9216;
+struct SamplerStage {
+  float *logits;   // [kStageMaxLogits]
+  uint64_t *seen;  // [129]
+  uint64_t *rng;
+  int32_t *tok;
+};
+// Looks up the staging array's address on device dev, which must be the current device;
+// later calls for the same device do nothing.
+hipError_t sampler_stage_init(int dev);
+// The staging area of device dev; false if sampler_stage_init has not run for it.
+bool sampler_stage(int dev, SamplerStage *out);
+
 // ---- Stage-2 CFM DiT estimator (kernels_cfm.hip); activations [B][T][C] fp32 ----
 hipError_t cfm_temb(const float *t, int B, float *emb /*[B][256]*/, hipStream_t s);
 hipError_t cfm_silu(const float *x, float *y, int n, hipStream_t s);

@@ -1,5 +1,7 @@
 // On-device sampler: sample_next_token (sampler.rs:191-284) in one 1024-thread block; the
 // algorithm and its bit-exactness argument are in sampler_core.h.
+#include <mutex>
+
 #include "kernels.h"
 #include "sampler_core.h"
 
@@ -39,7 +41,46 @@ __global__ __launch_bounds__(kThreads) void sampler_kernel(float *logits, int n,
   }
 }
 
+// ---- staging without allocation ----------------------------------------------------
+// Byte offsets inside the staging array: logits, seen words, RNG state, token.
+constexpr size_t kStageSeenOff = sizeof(float) * kStageMaxLogits;
+constexpr size_t kStageRngOff = kStageSeenOff + sizeof(uint64_t) * 129;
+constexpr size_t kStageTokOff = kStageRngOff + sizeof(uint64_t);
+constexpr size_t kStageBytes = (kStageTokOff + sizeof(int32_t) + 255) / 256 * 256;  // 38144
+static_assert(kStageMaxLogits <= kThreads * kPerThread, "the sampler block must cover the staging area");
+
+// In host code `scratch` names a host-side stand-in, not device memory: host code uses the
+// address hipGetSymbolAddress returns for each device (g_stage_dev), never the name.
+static __device__ __align__(256) unsigned char scratch[kStageBytes];
+
+std::mutex g_stage_mu;
+char *g_stage_dev[kMaxDevices];  // per-device address of `scratch`
+
 }  // namespace
+
+hipError_t sampler_stage_init(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  if (g_stage_dev[dev]) return hipSuccess;
+  void *ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!ptr) return hipErrorInvalidSymbol;
+  g_stage_dev[dev] = static_cast<char *>(ptr);
+  return hipSuccess;
+}
+
+bool sampler_stage(int dev, SamplerStage *out) {
+  if (dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_stage_mu);
+  char *base = g_stage_dev[dev];
+  if (!base) return false;
+  out->logits = reinterpret_cast<float *>(base);
+  out->seen = reinterpret_cast<uint64_t *>(base + kStageSeenOff);
+  out->rng = reinterpret_cast<uint64_t *>(base + kStageRngOff);
+  out->tok = reinterpret_cast<int32_t *>(base + kStageTokOff);
+  return true;
+}
 
 hipError_t sampler_init() {
   // candidate sort keys for top_k up to 8194 need 128 KiB of LDS

@@ -24,7 +24,6 @@ using namespace itts;
 namespace {
 
 thread_local std::string g_last_error;
-constexpr int kMaxDevices = 64;  // device ordinals the library accepts
 
 itts_status set_error(itts_status st, const char *fmt, ...) {
   char buf[512];
@@ -954,6 +953,8 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
     g->device = dev;
     g->persist_ok = (bits == 8 || bits == 4) && coop != 0 && persist_init() == hipSuccess;
+    if (sampler_stage_init(dev) != hipSuccess)
+      return fail(set_error(ITTS_E_DEVICE, "sampler staging area lookup failed"));
   }
   if (g->gws.ensure(sizeof(float) * gemm_ws_floats(g->n_cu)) || g->gcnt.ensure(sizeof(uint32_t) * kGemmCounters) ||
       hipMemset(g->gcnt.p, 0, sizeof(uint32_t) * kGemmCounters) || gemm_init() != hipSuccess)
@@ -1268,6 +1269,34 @@ itts_status itts_sample_next_token(itts_gpt *gpt, float *logits, int32_t n, cons
   HIP_TRY(hipMemcpyAsync(logits, gpt->s_logits.p, sizeof(float) * n, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(rng_state, gpt->s_rng.p, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(token_out, gpt->s_tok.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return ITTS_OK;
+}
+
+// Calls on one device share its staging area: they are serialised here (each call
+// returns only after its copies back have completed).
+std::mutex g_stage_call_mu[kMaxDevices];
+
+itts_status itts_sample_next_token_noalloc(itts_gpt *gpt, float *logits, int32_t n, const uint64_t seen[129],
+                                           const itts_sampling *p, uint64_t *rng_state, int32_t *token_out) {
+  if (!gpt || !logits || !seen || !rng_state || !token_out)
+    return set_error(ITTS_E_VALIDATION, "logits: null argument");
+  if (n <= 0) return set_error(ITTS_E_VALIDATION, "logits: logits slice must not be empty");
+  if (n > kStageMaxLogits)
+    return set_error(ITTS_E_VALIDATION, "logits: at most %d logits (the size of the staging area)", kStageMaxLogits);
+  if (itts_status st = itts_sampling_validate(p)) return st;
+  SamplerStage sg{};
+  if (!sampler_stage(gpt->device, &sg))
+    return set_error(ITTS_E_DEVICE, "sampler staging area of device %d is not set up", gpt->device);
+  std::lock_guard<std::mutex> lock(g_stage_call_mu[gpt->device]);
+  hipStream_t s = gpt->stream;
+  HIP_TRY(hipMemcpyAsync(sg.logits, logits, sizeof(float) * n, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(sg.seen, seen, sizeof(uint64_t) * 129, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(sg.rng, rng_state, sizeof(uint64_t), hipMemcpyHostToDevice, s));
+  HIP_TRY(launch_sampler(sg.logits, n, sg.seen, to_dev_sampling(*p, n), sg.rng, sg.tok, nullptr, nullptr, -1, 0, s));
+  HIP_TRY(hipMemcpyAsync(logits, sg.logits, sizeof(float) * n, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(rng_state, sg.rng, sizeof(uint64_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(token_out, sg.tok, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   return ITTS_OK;
 }

@@ -161,6 +161,9 @@ _SIGS = {
     "itts_sample_next_token": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
                                          C.POINTER(itts_sampling), C.POINTER(C.c_uint64),
                                          C.POINTER(C.c_int32)]),
+    "itts_sample_next_token_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                                 C.POINTER(itts_sampling), C.POINTER(C.c_uint64),
+                                                 C.POINTER(C.c_int32)]),
     "itts_generate_codes_after": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(itts_code_prompt),
                                             C.POINTER(itts_sampling), C.POINTER(C.c_uint64),
                                             C.c_void_p, C.c_int32, C.POINTER(C.c_int32)]),
@@ -475,6 +478,18 @@ def sample_next_token(gpt: Gpt, logits: np.ndarray, seen: SeenTokenBitSet,
     p = params.to_c()
     _check(lib.itts_sample_next_token(gpt._h, _ptr(logits), len(logits), _ptr(seen.words),
                                       C.byref(p), C.byref(rng.state), C.byref(tok)))
+    return tok.value
+
+
+def sample_next_token_noalloc(gpt: Gpt, logits: np.ndarray, seen: SeenTokenBitSet,
+                              params: SamplingParams, rng: SamplerRng) -> int:
+    """sample_next_token through the entry point that allocates no device memory (the
+    library's static staging array); `logits` is penalised in place."""
+    assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+    tok = C.c_int32()
+    p = params.to_c()
+    _check(lib.itts_sample_next_token_noalloc(gpt._h, _ptr(logits), len(logits), _ptr(seen.words),
+                                              C.byref(p), C.byref(rng.state), C.byref(tok)))
     return tok.value
 
 
