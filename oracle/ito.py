@@ -13,7 +13,7 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_build", "libitts_oracle.so")
+LIB_PATH = os.environ.get("ITO_LIB") or os.path.join(HERE, "_build", "libitts_oracle.so")
 
 ITO_OK, ITO_E_VALIDATION, ITO_E_CAPACITY, ITO_E_ALLOC = 0, 1, 4, 5
 ITO_F32, ITO_F64 = 0, 1
