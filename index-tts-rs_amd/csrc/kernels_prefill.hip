@@ -240,8 +240,8 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     }
   };
 
-  // (scale, bias) of this wave's columns and group sums of its rows, for the group in st
-  auto read_group = [&](const char *st) __attribute__((always_inline)) {
+  // (scale, bias) of this wave's columns, for the group in st
+  auto read_params = [&](const char *st) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int nr = wn * 32 * TN + j * 32 + (lane & 31);
@@ -255,6 +255,10 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       if constexpr (BITS == 4) sb.y = sb.y - 16.0f * sb.x;
       sbp[j] = sb;
     }
+  };
+  // ... and the group sums of its rows
+  auto read_group = [&](const char *st) __attribute__((always_inline)) {
+    read_params(st);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int rb = wm * 32 * TM + i * 32 + (lane >> 5) * 4;
@@ -271,6 +275,25 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
 #pragma unroll
         for (int e = 0; e < 16; e++)
           acc[i][j][e] = fmaf(sbp[j].x, P[i][j][e], fmaf(sbp[j].y, gsp[i][e >> 2][e & 3], acc[i][j][e]));
+  };
+
+  // The fold straight from the stage in LDS (128 x 128 tiles): the group sums of one M
+  // sub-tile at a time are held in registers, so the fold adds 16 registers to the
+  // partial tile instead of 32 (those tiles run at the 256-register limit).
+  auto apply_from = [&](const char *st, const floatx16(&P)[TM][TN]) __attribute__((always_inline)) {
+    read_params(st);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int rb = wm * 32 * TM + i * 32 + (lane >> 5) * 4;
+      floatx4 g[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) g[q] = *reinterpret_cast<const floatx4 *>(st + Sh::OFF_G + (rb + q * 8) * 4);
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+          acc[i][j][e] = fmaf(sbp[j].x, P[i][j][e], fmaf(sbp[j].y, g[e >> 2][e & 3], acc[i][j][e]));
+    }
   };
 
   auto stage = [&](int i) __attribute__((always_inline)) { return lds + (i % NS) * Sh::STAGE; };
@@ -296,8 +319,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
         // 128 x 128 tiles at two waves per SIMD: the group's affine is applied at once, so
         // only one partial tile is live (the other wave on the SIMD covers the MFMA latency)
         mma(stage(i), Pc);
-        read_group(stage(i));
-        apply(Pc);
+        apply_from(stage(i), Pc);
       } else {
         mma(stage(i), Pc);
         if (i > 0) apply(Pp);

@@ -56,3 +56,13 @@ def full_int4():
     W, g, M = _full({"quant_bits": 4}, 13)
     yield W, g, M
     g.close()
+
+
+@pytest.fixture(scope="session")
+def full_f32_params():
+    """The real shape with F32 group parameters, the dtype of the shipped checkpoint."""
+    import itts_hip as H
+
+    W, g, M = _full({"param_dtype": H.ITTS_F32}, 19)
+    yield W, g, M
+    g.close()

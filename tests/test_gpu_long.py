@@ -219,3 +219,26 @@ def test_prefill_heavy_all_rows(full_model):
     say(f"[gpu]   rows {got.shape[0]}: max |logit diff| {err.max():.3g} (median row {np.median(err):.3g})")
     assert got.shape == (4 * 547, 8194)
     assert err.max() < LOGIT_TOL and err.max() < 1e-4
+
+
+def test_f32_group_params_full_size(full_f32_params):
+    """The shipped checkpoint's dtype (F32 scales and biases, loader.rs:927-930) at the real
+    shape: a 535-row prefill (the 128 x 128 GEMM tiles), persistent decode steps, and a
+    long-context prefill_after with steps to 1734 keys, against the oracle."""
+    W, g, M = full_f32_params
+    say("[gpu] F32 group params, full size")
+    pr = synth.make_prompt(W.cfg, 32, 500, seed=7)
+    for kvt in (H.ITTS_F32, H.ITTS_BF16):
+        kv, okv = g.kv_cache(2048, kvt), M.kv(2048, kv_bf16=kvt == H.ITTS_BF16)
+        a = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
+        b = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)
+        worst = float(np.abs(a - b).max())
+        for i, t in enumerate(np.random.default_rng(8).integers(0, 8192, 6)):
+            worst = max(worst, float(np.abs(g.step(kv, int(t), i + 2) - M.step(okv, int(t), i + 2)).max()))
+        say(f"[gpu]   kv {kvt}: decode path {kv.decode_path()}, 535-row prefill + 6 steps max |logit diff| {worst:.3g}")
+        assert worst < LOGIT_TOL and worst < (1e-4 if kvt == H.ITTS_F32 else 5e-3)
+    pr2 = synth.make_prompt(W.cfg, 32, 200, seed=2)
+    codes = np.random.default_rng(22).integers(0, 8192, 1500).astype(np.int32)
+    rows = oracle_rows(M, pr2, codes, kv_bf16=True)
+    worst, keys = _checkpoints(g, H.ITTS_BF16, pr2, codes, rows, (1496,))
+    assert keys[-1] == 235 + 1499 and worst < LOGIT_TOL and worst < 5e-3
