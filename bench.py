@@ -66,52 +66,69 @@ def step_bytes(weight_bytes: int, L: int) -> int:
     return weight_bytes + KV_ROW_BYTES * L + KV_ROW_BYTES + 8194 * 4
 
 
-def cpu_baseline(W, prompt, sp, n_steps: int):
-    """The oracle (CPU restatement of the reference decoder) on the same weights and
-    prompt: prefill, then n_steps sampled decode steps; threads = host cores (<= 16)."""
+def cpu_baseline(W, prompt, sp, n_steps: int, prior):
+    """The oracle (CPU restatement of the reference decoder) on the same weights: the
+    prompt's prefill (CPU time to first token), then, from a cache holding the prompt and
+    `prior` (the GPU run's first codes, so the context is the workload's mean), n_steps
+    sampled decode steps; threads = host cores (<= 16)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import ito
 
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     ito.lib.ito_set_threads(threads)
     M = ito.Model(W)
-    kv = M.kv(2048, kv_bf16=True)
     t0 = time.perf_counter()
-    logits = M.prefill_after(kv, prompt.text_tokens, prompt.conds, prompt.lang_id)
+    M.prefill_after(M.kv(2048, kv_bf16=True), prompt.text_tokens, prompt.conds, prompt.lang_id)
     t_prefill = time.perf_counter() - t0
+    kv = M.kv(2048, kv_bf16=True)
+    prior = np.ascontiguousarray(prior, np.int32)
+    logits = M.prefill_after(kv, prompt.text_tokens, prompt.conds, prompt.lang_id, prior)
+    L0 = kv.valid_len()
     seen = ito.seen_init()
+    for t in prior.tolist():
+        ito.lib.ito_seen_insert(ito._p(seen), int(t))
     state = ito.lib.ito_rng_init(1234)
     t0 = time.perf_counter()
     for s in range(n_steps):
         logits[8193] = -np.inf
         tok, state = ito.sample_next_token(logits, seen, sp, state)
         ito.lib.ito_seen_insert(ito._p(seen), tok)
-        logits = M.step(kv, tok, s + 2)
+        logits = M.step(kv, tok, len(prior) + s + 2)
     t_dec = time.perf_counter() - t0
     return {
         "value": round(n_steps / t_dec, 3),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle (C restatement of gpt.rs/sampler.rs, fp32, bf16 KV) on the same "
-                  f"weights: prefill {kv.valid_len() - n_steps} rows then {n_steps} sampled "
-                  f"decode steps; prefill took {t_prefill * 1e3:.0f} ms (CPU time to first "
-                  f"token), decode {t_dec * 1e3 / n_steps:.1f} ms/token",
+        "sample": f"oracle (C restatement of gpt.rs/sampler.rs, fp32, bf16 KV) on the same weights: "
+                  f"{n_steps} sampled decode steps at {L0 + 1}..{L0 + n_steps} keys (the GPU "
+                  f"workload's mean context, after prefilling the prompt and the GPU run's first "
+                  f"{len(prior)} codes), {t_dec * 1e3 / n_steps:.1f} ms/token; the {L0 - len(prior)}-row "
+                  f"prompt prefill (CPU time to first token) took {t_prefill * 1e3:.0f} ms",
         "ttft_ms": round(t_prefill * 1e3, 1),
     }
 
 
+def source_hash() -> str:
+    """sha256 of the persistent step kernel's source (the GPU box has no git metadata)."""
+    import hashlib
+    with open(os.path.join(ROOT, "index-tts-rs_amd", "csrc", "kernels_persist.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def measured_traffic(decode_path):
     """HBM bytes per launch of the persistent step from the committed rocprofv3 counter
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), with whether it was
+    measured on the kernel source built here; None if there is no summary."""
     if decode_path != "persistent":
-        return None
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_persist_traffic.json")
+        return None, None
+    path = os.path.join(ROOT, "profiles", "decode_persist_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)["hbm_bytes_per_launch"]
+            prof = json.load(f)
+        return prof["hbm_bytes_per_launch"], prof.get("kernel_source_sha256_16") == source_hash()
     except (OSError, KeyError, ValueError):
-        return None
+        return None, None
 
 
 def prefill_heavy(H, synth, g, cfg, seed):
@@ -140,6 +157,29 @@ def prefill_heavy(H, synth, g, cfg, seed):
             "bound": "mfma", "peak_tflops": 2500.0,
             "frac": round(tflop / (ms * 1e-3) / 2500.0, 4),
             "note": "fp16 MFMA with hi/lo split activations (two products per weight)"}
+
+
+def short_decode(H, synth, g, cfg, seed):
+    """The short workload (config 1): prefill 32 cond + 64 text (99 rows), 128 greedy steps
+    (penalty 10, STOP masked), bf16 cache; median of 5 generations, host call time."""
+    n_cond, n_text, n_steps, samp, bits, desc = WORKLOADS["short"]
+    pr = synth.make_prompt(cfg, n_cond, n_text, seed=seed + 1)
+    sp = H.SamplingParams(max_mel_tokens=n_steps, **samp)
+    cp = H.CodePrompt(pr.text_tokens, pr.conds, pr.lang_id, None, n_steps)
+    kv = g.kv_cache(2048, H.ITTS_BF16)
+    H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(0))
+    times, steps = [], []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        codes = H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(0))
+        times.append((time.perf_counter() - t0) * 1e3)
+        t = kv.last_timing()
+        steps.append(t["decode_ms"] / t["decode_steps"])
+    ms = statistics.median(times)
+    print(f"[bench] short decode: {n_steps / (ms * 1e-3):.1f} tokens/s", file=sys.stderr, flush=True)
+    return {"workload": desc, "tokens": len(codes), "ms": round(ms, 3),
+            "tokens_per_s": round(n_steps / (ms * 1e-3), 1),
+            "decode_step_us": round(statistics.median(steps) * 1e3, 2)}
 
 
 def batch_decode(H, synth, g, cfg, seed):
@@ -258,13 +298,14 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="long", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--cpu-steps", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prefill-heavy (4 x 547 rows) and int4 decode measurements")
-    ap.add_argument("--only", choices=["prefill", "prefill-heavy", "batch8", "cfm"],
-                    help="for profilers: only repeat the workload's prefill or the prefill-heavy "
-                         "forward --repeat times, print one line per call, no JSON")
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill-heavy", "batch8", "cfm"],
+                    help="for profilers: only repeat the workload's whole generation (decode), its "
+                         "prefill or the prefill-heavy forward --repeat times, print one line per "
+                         "call, no JSON")
     ap.add_argument("--repeat", type=int, default=6)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--decode", default="auto", choices=["auto", "multi", "persistent"],
@@ -301,6 +342,15 @@ def main():
         if args.only == "batch8":
             r = batch_decode(H, synth, g, cfg, args.seed)
             print(f"[bench] batch8: {r['aggregate_tokens_per_s']} tokens/s aggregate", flush=True)
+            return
+        if args.only == "decode":
+            sp = H.SamplingParams(max_mel_tokens=n_steps, **samp)
+            cp = H.CodePrompt(prompt.text_tokens, prompt.conds, prompt.lang_id, None, n_steps)
+            for i in range(args.repeat):
+                t0 = time.perf_counter()
+                codes = H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(1234))
+                print(f"[bench] decode generation {i}: {len(codes)} codes in "
+                      f"{(time.perf_counter() - t0) * 1e3:.2f} ms", flush=True)
             return
         for i in range(args.repeat):
             t0 = time.perf_counter()
@@ -373,7 +423,7 @@ def main():
     achieved = bytes_step / (kernel_ms * 1e-3) / 1e9
     kernel_name = ("decode_persist_kernel (one launch = one decode step)" if decode_path == "persistent"
                    else "decode step (122 kernels)")
-    traffic = measured_traffic(decode_path)
+    traffic, traffic_current = measured_traffic(decode_path)
     value = args.steps * n_tok / wall
     out = {
         "metric": METRIC,
@@ -400,18 +450,21 @@ def main():
         "decode_kernel_us": round(kernel_ms * 1e3, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": kernel_name,
+                     "traffic": traffic, "traffic_measured_on_this_kernel_source": traffic_current,
+                     "kernel": kernel_name,
                      "bytes_per_launch": bytes_step, "mean_keys": mean_L},
     }
     if not args.no_secondary and args.workload == "long":
-        out["secondary"] = {"prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed),
+        out["secondary"] = {"short_decode": short_decode(H, synth, g, cfg, args.seed),
+                            "prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed),
                             "batch8_decode": batch_decode(H, synth, g, cfg, args.seed)}
         del g, kv
         out["secondary"]["int4_decode"] = int4_decode(H, synth, args.seed)
         out["secondary"]["cfm_solve"] = cfm_solve(args.seed)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(W, prompt, sp, args.cpu_steps)
+        n_prior = max(0, int(round(mean_L)) - T)
+        out["cpu_baseline"] = cpu_baseline(W, prompt, sp, args.cpu_steps, codes[:n_prior])
     print(json.dumps(out), flush=True)
 
 
