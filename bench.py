@@ -13,9 +13,10 @@ replay of the captured sample+step graph) is the unit whose HBM roofline is repo
 achieved = algorithmic bytes of one decode step / its average device time (HIP events
 on the decoder's stream).
 
-The default run also reports, under "secondary", the prefill-heavy workload (4 x 547
-rows, all-row logits, MFMA-bound), the batch-8 decode workload, the int4 decode
-workload and the Stage-2 CFM estimator's 25-step solve for 10 s of audio.
+The default run also reports, under "secondary", the short workload, the long workload
+with an fp32 cache, the prefill-heavy workload (4 x 547 rows, all-row logits,
+MFMA-bound), the batch-8 decode workload, the int4 decode workload and the Stage-2 CFM
+estimator's 25-step solve for 10 s of audio.
 
 Usage: python bench.py [--steps K] [--warmup W] [--workload long|short|int4]
 """
@@ -182,6 +183,25 @@ def short_decode(H, synth, g, cfg, seed):
             "decode_step_us": round(statistics.median(steps) * 1e3, 2)}
 
 
+def f32_kv_decode(H, g, cp, sp, weight_bytes):
+    """The long workload with the reference's fp32 cache instead of bf16 (twice the KV
+    bytes per key): one warm-up and one timed generation, device-timed decode rate."""
+    kv = g.kv_cache(2048, H.ITTS_F32)
+    path = "persistent" if kv.decode_path() == H.ITTS_DECODE_PERSISTENT else "multi-kernel"
+    H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(1234))
+    codes = H.generate_codes_after(g, cp, kv, sp, H.SamplerRng(1234))
+    t = kv.last_timing()
+    step_ms = t["decode_ms"] / t["decode_steps"]
+    mean_L = int(round(t["prefill_rows"] + (t["decode_steps"] + 1) / 2.0))
+    nbytes = step_bytes(weight_bytes, mean_L) + KV_ROW_BYTES * (mean_L + 1)  # f32 rows: twice bf16's
+    achieved = nbytes / (step_ms * 1e-3) / 1e9
+    print(f"[bench] f32-cache decode: {1e3 / step_ms:.1f} tokens/s ({path})", file=sys.stderr, flush=True)
+    kv.close()
+    return {"workload": "the long workload with an fp32 KV cache", "decode_path": path, "tokens": int(len(codes)),
+            "decode_tokens_per_s": round(1e3 / step_ms, 2), "decode_step_us": round(step_ms * 1e3, 2),
+            "hbm_achieved_gbs": round(achieved, 1), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)}
+
+
 def batch_decode(H, synth, g, cfg, seed):
     """The batched workload: 8 sentences with text lengths U[20, 200] and decode lengths
     U[200, 1200] (seeded), each stopping at its own length (STOP masked until then),
@@ -310,6 +330,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--decode", default="auto", choices=["auto", "multi", "persistent"],
                     help="decode-step implementation (auto: persistent where supported)")
+    ap.add_argument("--kv", default="bf16", choices=["bf16", "f32"],
+                    help="KV cache rows for --only decode / prefill")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the decoder runs one sequence per GPU and this "
@@ -330,7 +352,7 @@ def main():
     g = H.Gpt(W)
     if args.only:
         prompt = synth.make_prompt(cfg, n_cond, n_text, seed=args.seed + 1)
-        kv = g.kv_cache(2048, H.ITTS_BF16)
+        kv = g.kv_cache(2048, H.ITTS_BF16 if args.kv == "bf16" else H.ITTS_F32)
         heavy = []
         for b in range(4):
             pr = synth.make_prompt(cfg, 32, 512, seed=args.seed + 10 + b)
@@ -456,6 +478,7 @@ def main():
     }
     if not args.no_secondary and args.workload == "long":
         out["secondary"] = {"short_decode": short_decode(H, synth, g, cfg, args.seed),
+                            "f32_kv_decode": f32_kv_decode(H, g, cp, sp, weight_bytes),
                             "prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed),
                             "batch8_decode": batch_decode(H, synth, g, cfg, args.seed)}
         del g, kv

@@ -174,8 +174,9 @@ struct PersistArgs {
   DevQL head;
   const float *ln_f_w, *ln_f_b, *fn_w, *fn_b;
   const float *mel_emb, *mel_pos;
-  void *kc, *vc;           // bf16 cache bases [n_layer][H][max_seq][64]
+  void *kc, *vc;           // cache bases [n_layer][H][max_seq][64], bf16 or f32 rows
   int max_seq;
+  int kvt;                 // KvType of the rows
   DecodeCtl *ctl;
   // exchange arrays of 16-byte words (three values and an epoch), 16-byte aligned
   void *x_x, *x_qkv, *x_part, *x_attn, *x_mid, *x_f;
@@ -188,15 +189,19 @@ struct PersistArgs {
   int xin_len, part_len, own_len, out_len, pp_len, lp_len;
 };
 // Whether the persistent step supports this shape on B blocks; *S = attention splits.
+// f32 rows also need persist_f32_v_floats() floats from the start of the block's LDS
+// (input row, normalised row and partials: the host pads the partials to fit).
 bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int bits, int *S);
 constexpr size_t kPersistMaxLds = 150 * 1024;
+// LDS floats that f32 V rows of one attention split take: 512 per chunk of 8 keys.
+inline int persist_f32_v_floats(int max_seq, int S) { return 512 * (((max_seq + S - 1) / S + 7) / 8); }
 size_t persist_lds_bytes(const PersistArgs &a);
 // 16-byte words of the exchange arrays x_x, x_qkv, x_part, x_attn, x_mid, x_f: total, and
 // each array's offset in off[6].
 size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]);
 // Whether one block of the persistent kernel with `lds` bytes of dynamic LDS fits a
 // compute unit (threads, static + dynamic LDS).
-hipError_t persist_fits(int bits, int ptype, size_t lds, bool *fits);
+hipError_t persist_fits(int bits, int ptype, int kvt, size_t lds, bool *fits);
 hipError_t launch_decode_persist(PersistArgs a, int bits, int ptype, hipStream_t s);
 // Raises the kernel's dynamic-LDS limit; once per process, outside stream capture.
 hipError_t persist_init();

@@ -480,7 +480,7 @@ enum Role : int { kRolePoll = 0, kRolePub = 1, kRoleLoad = 2 };
 // sequence of __syncthreads; each contains only its role's work, so the compiler allocates
 // registers per role (a role branch on a divergent condition would be linearised and make
 // every wave hold the registers of all roles).
-template <int BITS, int PT, int ROLE>
+template <int BITS, int PT, int KVF, int ROLE>
 __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, float *lds) {
   constexpr bool poller = ROLE == kRolePoll, pub = ROLE == kRolePub, loader = ROLE == kRoleLoad;
   DecodeCtl *ctl = a.ctl;
@@ -583,8 +583,11 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
         if (R >= d) {
           const int idx = R < 2 * d ? R - d : R - 2 * d;
           const int h = idx >> 6, e = idx & 63;
-          uint16_t *cache = static_cast<uint16_t *>(R < 2 * d ? a.kc : a.vc);
-          cache[(((size_t)l * H + h) * a.max_seq + vlen) * 64 + e] = (uint16_t)float_to_bf16_bits(out[r]);
+          const size_t at = (((size_t)l * H + h) * a.max_seq + vlen) * 64 + e;
+          if constexpr (KVF)
+            static_cast<float *>(R < 2 * d ? a.kc : a.vc)[at] = out[r];
+          else
+            static_cast<uint16_t *>(R < 2 * d ? a.kc : a.vc)[at] = (uint16_t)float_to_bf16_bits(out[r]);
         }
       }
     }
@@ -597,22 +600,45 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // ---------------- P2: attention split of head ah over keys [j0, j1) ----------------
     if (attn_block) {
       // cached K/V rows of the split (the appended row comes from the exchange), copied
-      // straight into LDS (no registers) before the query arrives; out-of-split slots read
-      // row 0.  Lane ll of pass ps lands at kvs[(ps*576 + ll)*4], K passes then V passes.
+      // straight into LDS (no registers) before the query arrives.  Wave lw of pass ps
+      // holds the split's keys 8c .. 8c+7, c = 9 ps + lw (8 lanes per key, each lane 8
+      // dimensions); slots past the split or at the appended row read row 0.  bf16 rows:
+      // lane ll of pass ps lands at kvs[(ps*576 + ll)*4], K passes then V passes.  f32 rows
+      // (twice the bytes): K in kvs and V in the input-row / normalised-row / partials
+      // area, which nothing uses between P1's row sums and P3's all-gather; each 8-key
+      // chunk c is two 1 KB halves (dimensions 0-3 and 4-7 of every lane's slice), lane
+      // at [(2c + half)*256 + lane*4], and a wave whose keys all lie past the split copies
+      // nothing (the V area holds only the chunks a split can reach).
       if (loader) {
         const size_t hb = ((size_t)l * H + ah) * a.max_seq * 64;
-        const uint16_t *kh = static_cast<const uint16_t *>(a.kc) + hb;
-        const uint16_t *vh = static_cast<const uint16_t *>(a.vc) + hb;
 #pragma unroll
         for (int ps = 0; ps < kKeyPasses; ps++) {
+          const int c = ps * kLoadWaves + lw;
+          if (KVF && 8 * c >= j1 - j0) continue;
           int key = j0 + kslot + kKeySlots * ps;
           key = key < j1 && key < L - 1 ? key : 0;
-          float *wk = kvs + (ps * kLoadThreads + lw * 64) * 4;
-          float *wv = kvs + ((kKeyPasses + ps) * kLoadThreads + lw * 64) * 4;
-          __builtin_amdgcn_global_load_lds(kh + (size_t)key * 64 + dsl * 8, (__attribute__((address_space(3))) void *)wk,
-                                           16, 0, 0);
-          __builtin_amdgcn_global_load_lds(vh + (size_t)key * 64 + dsl * 8, (__attribute__((address_space(3))) void *)wv,
-                                           16, 0, 0);
+          if constexpr (KVF) {
+            const float *kh = static_cast<const float *>(a.kc) + hb + (size_t)key * 64 + dsl * 8;
+            const float *vh = static_cast<const float *>(a.vc) + hb + (size_t)key * 64 + dsl * 8;
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+              __builtin_amdgcn_global_load_lds(kh + 4 * hf,
+                                               (__attribute__((address_space(3))) void *)(kvs + (2 * c + hf) * 256),
+                                               16, 0, 0);
+              __builtin_amdgcn_global_load_lds(vh + 4 * hf,
+                                               (__attribute__((address_space(3))) void *)(xin + (2 * c + hf) * 256),
+                                               16, 0, 0);
+            }
+          } else {
+            const uint16_t *kh = static_cast<const uint16_t *>(a.kc) + hb;
+            const uint16_t *vh = static_cast<const uint16_t *>(a.vc) + hb;
+            float *wk = kvs + (ps * kLoadThreads + lw * 64) * 4;
+            float *wv = kvs + ((kKeyPasses + ps) * kLoadThreads + lw * 64) * 4;
+            __builtin_amdgcn_global_load_lds(kh + (size_t)key * 64 + dsl * 8,
+                                             (__attribute__((address_space(3))) void *)wk, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vh + (size_t)key * 64 + dsl * 8,
+                                             (__attribute__((address_space(3))) void *)wv, 16, 0, 0);
+          }
         }
       }
       if (poller) {
@@ -667,8 +693,8 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       }
       __syncthreads();
       if (sh.abort) return;
-      // the appended row as the cache stores it (bf16)
-      if (pub) {
+      // the appended row as the cache stores it (bf16 rows round it)
+      if (pub && !KVF) {
         kn[lane] = bf16_bits_to_float(float_to_bf16_bits(kn[lane]));
         vn[lane] = bf16_bits_to_float(float_to_bf16_bits(vn[lane]));
       }
@@ -686,6 +712,19 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
             if (key == L - 1) {
 #pragma unroll
               for (int e = 0; e < 8; e++) pd += qs[dsl * 8 + e] * kn[dsl * 8 + e];
+            } else if constexpr (KVF) {
+              const int c = ps * kLoadWaves + lw;
+              const float4 k0 = *reinterpret_cast<const float4 *>(kvs + 2 * c * 256 + lane * 4);
+              const float4 k1 = *reinterpret_cast<const float4 *>(kvs + (2 * c + 1) * 256 + lane * 4);
+              const float *qq = qs + dsl * 8;
+              pd += qq[0] * k0.x;
+              pd += qq[1] * k0.y;
+              pd += qq[2] * k0.z;
+              pd += qq[3] * k0.w;
+              pd += qq[4] * k1.x;
+              pd += qq[5] * k1.y;
+              pd += qq[6] * k1.z;
+              pd += qq[7] * k1.w;
             } else {
               const uint4 kq = *reinterpret_cast<const uint4 *>(kvs + (ps * kLoadThreads + ll) * 4);
               const uint32_t w[4] = {kq.x, kq.y, kq.z, kq.w};
@@ -725,6 +764,18 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
             if (key == L - 1) {
 #pragma unroll
               for (int e = 0; e < 8; e++) o8[e] += p * vn[dsl * 8 + e];
+            } else if constexpr (KVF) {
+              const int c = ps * kLoadWaves + lw;
+              const float4 v0 = *reinterpret_cast<const float4 *>(xin + 2 * c * 256 + lane * 4);
+              const float4 v1 = *reinterpret_cast<const float4 *>(xin + (2 * c + 1) * 256 + lane * 4);
+              o8[0] += p * v0.x;
+              o8[1] += p * v0.y;
+              o8[2] += p * v0.z;
+              o8[3] += p * v0.w;
+              o8[4] += p * v1.x;
+              o8[5] += p * v1.y;
+              o8[6] += p * v1.z;
+              o8[7] += p * v1.w;
             } else {
               const uint4 vq = *reinterpret_cast<const uint4 *>(kvs + ((kKeyPasses + ps) * kLoadThreads + ll) * 4);
               const uint32_t w[4] = {vq.x, vq.y, vq.z, vq.w};
@@ -889,7 +940,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   }
 }
 
-template <int BITS, int PT>
+template <int BITS, int PT, int KVF>
 __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a) {
   __shared__ PersistShared sh;
   extern __shared__ float lds[];
@@ -900,19 +951,23 @@ __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a)
   }
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (wave >= kLoadWave0)
-    run<BITS, PT, kRoleLoad>(a, sh, lds);
+    run<BITS, PT, KVF, kRoleLoad>(a, sh, lds);
   else if (wave == kPubWave)
-    run<BITS, PT, kRolePub>(a, sh, lds);
+    run<BITS, PT, KVF, kRolePub>(a, sh, lds);
   else
-    run<BITS, PT, kRolePoll>(a, sh, lds);
+    run<BITS, PT, KVF, kRolePoll>(a, sh, lds);
 }
 
-const void *persist_fn(int bits, int ptype) {
+template <int BITS, int PT>
+const void *persist_fn_kv(int kvt) {
+  return kvt == kKvF32 ? reinterpret_cast<const void *>(decode_persist_kernel<BITS, PT, 1>)
+                       : reinterpret_cast<const void *>(decode_persist_kernel<BITS, PT, 0>);
+}
+
+const void *persist_fn(int bits, int ptype, int kvt) {
   if (bits == 4)
-    return ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<4, kParamF16>)
-                              : reinterpret_cast<const void *>(decode_persist_kernel<4, kParamF32>);
-  return ptype == kParamF16 ? reinterpret_cast<const void *>(decode_persist_kernel<8, kParamF16>)
-                            : reinterpret_cast<const void *>(decode_persist_kernel<8, kParamF32>);
+    return ptype == kParamF16 ? persist_fn_kv<4, kParamF16>(kvt) : persist_fn_kv<4, kParamF32>(kvt);
+  return ptype == kParamF16 ? persist_fn_kv<8, kParamF16>(kvt) : persist_fn_kv<8, kParamF32>(kvt);
 }
 
 }  // namespace
@@ -962,21 +1017,22 @@ size_t persist_lds_bytes(const PersistArgs &a) {
 hipError_t launch_decode_persist(PersistArgs a, int bits, int ptype, hipStream_t s) {
   void *args[] = {&a};
   const size_t lds = persist_lds_bytes(a);
-  return hipLaunchKernel(persist_fn(bits, ptype), dim3(a.B), dim3(kThreads), args, lds, s);
+  return hipLaunchKernel(persist_fn(bits, ptype, a.kvt), dim3(a.B), dim3(kThreads), args, lds, s);
 }
 
 hipError_t persist_init() {
   for (int bits : {8, 4})
-    for (int pt : {kParamF16, kParamF32}) {
-      hipError_t e = hipFuncSetAttribute(persist_fn(bits, pt), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)kPersistMaxLds);
-      if (e != hipSuccess) return e;
-    }
+    for (int pt : {kParamF16, kParamF32})
+      for (int kvt : {kKvBf16, kKvF32}) {
+        hipError_t e = hipFuncSetAttribute(persist_fn(bits, pt, kvt), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)kPersistMaxLds);
+        if (e != hipSuccess) return e;
+      }
   return hipSuccess;
 }
 
-hipError_t persist_fits(int bits, int ptype, size_t lds, bool *fits) {
-  const void *fn = persist_fn(bits, ptype);
+hipError_t persist_fits(int bits, int ptype, int kvt, size_t lds, bool *fits) {
+  const void *fn = persist_fn(bits, ptype, kvt);
   hipFuncAttributes fa{};
   hipError_t e = hipFuncGetAttributes(&fa, fn);
   if (e != hipSuccess) return e;

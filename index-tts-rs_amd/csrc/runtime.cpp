@@ -747,7 +747,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
   *used = false;
   const itts_config &c = g->cfg;
   int S = 0;
-  const bool shape_ok = g->persist_ok && kv->kvt == kKvBf16 &&
+  const bool shape_ok = g->persist_ok &&
                         persist_supported(c.d_model, c.d_ffn, c.mel_vocab, c.n_head, c.n_layer, kv->max_seq,
                                           g->n_cu, c.quant_bits, &S);
   PersistArgs a{};
@@ -770,14 +770,18 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     a.out_len = r4(std::max({rq, rp, rf, rh}));
     a.pp_len = r4(S * 66);
     a.lp_len = r4(4 * d + std::max(rq + rp + rf + rp, rh));
+    a.kvt = kv->kvt;
+    // f32 rows: V of a split is staged over the input row, normalised row and partials
+    if (kv->kvt == kKvF32)
+      a.part_len = std::max(a.part_len, r4(persist_f32_v_floats(kv->max_seq, S) - a.xin_len - d));
   }
   bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
-  if (ok) HIP_TRY(persist_fits(c.quant_bits, g->ptype(), persist_lds_bytes(a), &ok));  // one block per CU
+  if (ok) HIP_TRY(persist_fits(c.quant_bits, g->ptype(), kv->kvt, persist_lds_bytes(a), &ok));  // one block per CU
   if (g->path == ITTS_DECODE_PERSISTENT && !ok)
     return set_error(ITTS_E_VALIDATION,
-                     "decode_path: the persistent decode step does not support this cache (bf16 rows, "
+                     "decode_path: the persistent decode step does not support this cache (%s rows, "
                      "max_seq %d, %d compute units)",
-                     kv->max_seq, B);
+                     kv->kvt == kKvBf16 ? "bf16" : "f32", kv->max_seq, B);
   if (!ok || g->path == ITTS_DECODE_MULTI) return ITTS_OK;
   size_t off[6];
   const size_t words = persist_exchange_words(d, F, H, S, B, off);

@@ -25,8 +25,8 @@ def say(*a):
     sys.stdout.flush()
 
 
-# "persistent" runs AUTO, which picks the persistent step for every bf16 cache here (and
-# the multi-kernel step for fp32 caches); "multi" forces the multi-kernel step.
+# "persistent" runs AUTO, which picks the persistent step for every cache here (bf16 and
+# fp32 rows); "multi" forces the multi-kernel step.
 PATHS = {"persistent": H.ITTS_DECODE_AUTO, "multi": H.ITTS_DECODE_MULTI}
 
 
@@ -44,8 +44,7 @@ def model(request):
 
 
 def expect_path(g, kv, kvt=H.ITTS_BF16):
-    want = g.path if kvt == H.ITTS_BF16 else H.ITTS_DECODE_MULTI
-    assert kv.decode_path() == want
+    assert kv.decode_path() == g.path
 
 
 @pytest.mark.parametrize("kvt", [H.ITTS_BF16, H.ITTS_F32])
@@ -214,15 +213,22 @@ def test_validation_and_capacity_errors(model):
     assert kv.valid_len() == 32
 
 
-def test_forced_persistent_rejects_fp32_cache(model):
+def test_forced_persistent_cache_shapes(model):
+    """Forced persistent step: bf16 and fp32 caches take it; a cache longer than the
+    step's key slots hold (12 splits x 216 keys) is rejected, and AUTO gives it the
+    multi-kernel step."""
     W, g, _ = model
     if g.path != H.ITTS_DECODE_PERSISTENT:
         pytest.skip("persistent-path case")
     g.set_decode_path(H.ITTS_DECODE_PERSISTENT)
     try:
-        with pytest.raises(H.ValidationError) as e:
-            g.kv_cache(64, H.ITTS_F32)
-        assert e.value.message.startswith("decode_path")
+        assert g.kv_cache(64, H.ITTS_F32).decode_path() == H.ITTS_DECODE_PERSISTENT
+        assert g.kv_cache(2048, H.ITTS_F32).decode_path() == H.ITTS_DECODE_PERSISTENT
         assert g.kv_cache(64).decode_path() == H.ITTS_DECODE_PERSISTENT
+        with pytest.raises(H.ValidationError) as e:
+            g.kv_cache(12 * 216 + 1)
+        assert e.value.message.startswith("decode_path")
+        g.set_decode_path(H.ITTS_DECODE_AUTO)
+        assert g.kv_cache(12 * 216 + 1).decode_path() == H.ITTS_DECODE_MULTI
     finally:
         g.set_decode_path(H.ITTS_DECODE_AUTO)

@@ -89,6 +89,7 @@ def test_long_utterance(full_model, kv_dtype):
     pr = synth.make_prompt(W.cfg, 32, 200, seed=2)
     sp, st0, st_end, codes, kv = _generate(g, pr, 1500, SAMPLED, kv_dtype, 1234)
     say(f"[gpu]   decode path {kv.decode_path()}, cache {kv.valid_len()} rows; oracle rows ...")
+    assert kv.decode_path() == H.ITTS_DECODE_PERSISTENT
     rows = oracle_rows(M, pr, codes, kv_bf16=kv_dtype == H.ITTS_BF16)
     _dump(f"long_{kv_dtype}", codes=codes, st0=st0, st_end=st_end)
     worst, keys = _checkpoints(g, kv_dtype, pr, codes, rows, (640, 1065, 1496))
@@ -98,19 +99,20 @@ def test_long_utterance(full_model, kv_dtype):
     _check_stream(rows, codes, sp, st0, st_end, eps=4 * worst, max_mism=15 if kv_dtype == H.ITTS_BF16 else 2)
 
 
-def test_long_utterance_multi_kernel_steps(full_model):
-    """The multi-kernel decode step (bf16 cache) at the same long contexts."""
+@pytest.mark.parametrize("kv_dtype", [H.ITTS_BF16, H.ITTS_F32], ids=["bf16", "f32"])
+def test_long_utterance_multi_kernel_steps(full_model, kv_dtype):
+    """The multi-kernel decode step at the same long contexts."""
     W, g, M = full_model
-    say("[gpu] long contexts, multi-kernel step, bf16")
+    say(f"[gpu] long contexts, multi-kernel step, kv {'bf16' if kv_dtype == H.ITTS_BF16 else 'f32'}")
     pr = synth.make_prompt(W.cfg, 32, 200, seed=2)
     codes = np.random.default_rng(21).integers(0, 8192, 1500).astype(np.int32)
-    rows = oracle_rows(M, pr, codes, kv_bf16=True)
+    rows = oracle_rows(M, pr, codes, kv_bf16=kv_dtype == H.ITTS_BF16)
     g.set_decode_path(H.ITTS_DECODE_MULTI)
     try:
-        worst, _ = _checkpoints(g, H.ITTS_BF16, pr, codes, rows, (640, 1496))
+        worst, _ = _checkpoints(g, kv_dtype, pr, codes, rows, (640, 1496))
     finally:
         g.set_decode_path(H.ITTS_DECODE_AUTO)
-    assert worst < LOGIT_TOL and worst < 5e-3
+    assert worst < LOGIT_TOL and worst < (5e-3 if kv_dtype == H.ITTS_BF16 else 1e-4)
 
 
 def test_int4_long(full_int4):
@@ -128,13 +130,20 @@ def test_int4_long(full_int4):
     _check_stream(rows, codes, sp, st0, st_end, eps=4 * worst, max_mism=15)
 
 
-def test_short_greedy_identical_f32(full_model):
-    """Config 1 with the reference's fp32 cache: all 128 greedy ids identical to the
-    oracle's decisions (and so to its free-running decode)."""
+@pytest.mark.parametrize("path", [H.ITTS_DECODE_AUTO, H.ITTS_DECODE_MULTI], ids=["persistent", "multi"])
+def test_short_greedy_identical_f32(full_model, path):
+    """Config 1 with the reference's fp32 cache, on the persistent step (what AUTO picks)
+    and on the multi-kernel step: all 128 greedy ids identical to the oracle's decisions
+    (and so to its free-running decode)."""
     W, g, M = full_model
-    say("[gpu] short 32+64, 128 greedy steps, f32")
+    say(f"[gpu] short 32+64, 128 greedy steps, f32, path {path}")
     pr = synth.make_prompt(W.cfg, 32, 64, seed=5)
-    sp, st0, st_end, codes, kv = _generate(g, pr, 128, GREEDY, H.ITTS_F32, 0)
+    g.set_decode_path(path)
+    try:
+        sp, st0, st_end, codes, kv = _generate(g, pr, 128, GREEDY, H.ITTS_F32, 0)
+        assert kv.decode_path() == (H.ITTS_DECODE_PERSISTENT if path == H.ITTS_DECODE_AUTO else H.ITTS_DECODE_MULTI)
+    finally:
+        g.set_decode_path(H.ITTS_DECODE_AUTO)
     rows = oracle_rows(M, pr, codes, kv_bf16=False)
     mism, _, _ = replay_stream(rows, codes, sp, st0, 128, STOP, 0.0)
     say(f"[gpu]   decode path {kv.decode_path()}; differing decisions {mism}")
