@@ -5,11 +5,10 @@
 // count), forward_merged -> itts_cfm_forward, solve_euler -> itts_cfm_solve_euler.  The
 // estimator keeps fp32 activations: its linears (and WaveNet's kernel-5 convolution, as one
 // GEMM over a zero-padded buffer whose operand rows overlap) run on the split-fp16 MFMA GEMM
-// of kernels_cfm.hip on the estimator's stream, products under 64 rows on rocBLAS sgemm;
-// the other kernels in kernels_cfm.hip do the rest.  Layout: activations [B][T][C] row-major, the CFG
+// of kernels_cfm.hip on the estimator's stream, products under 64 rows on its few-row fp32
+// product; the other kernels in kernels_cfm.hip do the rest.  Layout: activations [B][T][C] row-major, the CFG
 // pair as batch rows 0 (conditioned) and 1 (unconditioned).
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <cstdarg>
 #include <cstdio>
@@ -44,12 +43,6 @@ itts_status cerr(itts_status st, const char *fmt, ...) {
     hipError_t e_ = (expr);                                                                            \
     if (e_ != hipSuccess) return cerr(ITTS_E_DEVICE, "HIP error %s at %s:%d", hipGetErrorName(e_), __FILE__, __LINE__); \
   } while (0)
-#define BL(expr)                                                                                       \
-  do {                                                                                                 \
-    rocblas_status b_ = (expr);                                                                        \
-    if (b_ != rocblas_status_success)                                                                  \
-      return cerr(ITTS_E_DEVICE, "rocBLAS error %s at %s:%d", rocblas_status_to_string(b_), __FILE__, __LINE__); \
-  } while (0)
 
 constexpr int kFreqDim = 256;
 
@@ -77,29 +70,15 @@ struct Buf {
   }
 };
 
-// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart).  Row blocks of 64 and
-// more run on the split-fp16 MFMA GEMM on the handle's stream; smaller ones (the per-batch
-// timestep and style projections) and operands it cannot take go to rocBLAS as the
-// column-major product y^T = W A^T.  ITTS_CFM_ROCBLAS=1 sends every product to rocBLAS.
-bool force_rocblas() {
-  static const bool f = [] {
-    const char *e = std::getenv("ITTS_CFM_ROCBLAS");
-    return e && e[0] == '1';
-  }();
-  return f;
-}
-rocblas_status gemm(rocblas_handle h, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                    int ldy, float beta) {
-  if (M >= 64 && !force_rocblas() && itts::cfm_gemm_fits(A, lda, W, ldw, K)) {
-    hipStream_t st = nullptr;
-    if (rocblas_get_stream(h, &st) != rocblas_status_success) return rocblas_status_internal_error;
-    return itts::cfm_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st) == hipSuccess
-               ? rocblas_status_success
-               : rocblas_status_internal_error;
-  }
-  const float one = 1.0f;
-  return rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W, ldw, A, lda, &beta, y,
-                       ldy);
+// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart) on the estimator's
+// stream: row blocks of 64 and more on the split-fp16 MFMA GEMM, fewer rows (the per-batch
+// timestep, AdaLN and WaveNet-conditioning projections, forwards of under 64 frames) and
+// operands the MFMA GEMM cannot take on the few-row fp32 product.
+hipError_t gemm(hipStream_t st, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
+                int ldy, float beta) {
+  if (M >= 64 && itts::cfm_gemm_fits(A, lda, W, ldw, K))
+    return itts::cfm_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st);
+  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st);
 }
 
 struct Block {
@@ -114,7 +93,6 @@ struct WnLayer {
 struct itts_cfm {
   itts_cfm_config c{};
   hipStream_t s = nullptr;
-  rocblas_handle blas = nullptr;
   float *arena = nullptr;
   const float *cond_w, *cond_b, *merge_w, *merge_b;
   const float *te_w0[2], *te_b0[2], *te_w2[2], *te_b2[2];
@@ -134,7 +112,6 @@ struct itts_cfm {
   ~itts_cfm() {
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
-    if (blas) (void)rocblas_destroy_handle(blas);
     if (arena) (void)hipFree(arena);
     if (s) (void)hipStreamDestroy(s);
   }
@@ -196,10 +173,10 @@ itts_status timestep(itts_cfm *m, int e, int B, float *out) {
   hipStream_t s = m->s;
   CK(cfm_temb(m->tdev.p, B, m->emb.p, s));
   CK(cfm_bias_rows(m->th.p, d, m->te_b0[e], B, d, s));
-  BL(gemm(m->blas, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 1.0f));
+  CK(gemm(m->s, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 1.0f));
   CK(cfm_silu(m->th.p, m->th.p, B * d, s));
   CK(cfm_bias_rows(out, d, m->te_b2[e], B, d, s));
-  BL(gemm(m->blas, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 1.0f));
+  CK(gemm(m->s, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 1.0f));
   return ITTS_OK;
 }
 
@@ -211,22 +188,21 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
   const int MD = 2 * C + d + c.style_dim, R = B * T, Lc = c.n_layers, split = Lc / 2;
   const int na2 = (2 * Lc + 1) * 2 * d;  // packed AdaLN modulation width
   hipStream_t s = m->s;
-  rocblas_handle bl = m->blas;
   if (itts_status st = ensure_rows(m, B, T)) return st;
   // conditioning vectors: t1, t2, every AdaLN's (w, b), WaveNet's per-layer g, FinalLayer's (shift, scale)
   if (itts_status st = timestep(m, 0, B, m->t1.p)) return st;
   if (itts_status st = timestep(m, 1, B, m->t2.p)) return st;
   CK(cfm_bias_rows(m->mods.p, na2, m->ada_b, B, na2, s));
-  BL(gemm(bl, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 1.0f));
+  CK(gemm(s, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 1.0f));
   CK(cfm_bias_rows(m->wng.p, 2 * d * NL, m->wc_b, B, 2 * d * NL, s));
-  BL(gemm(bl, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 1.0f));
+  CK(gemm(s, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 1.0f));
   CK(cfm_silu(m->t1.p, m->st.p, B * d, s));
   CK(cfm_bias_rows(m->fmod.p, 2 * d, m->fa_b, B, 2 * d, s));
-  BL(gemm(bl, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 1.0f));
+  CK(gemm(s, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 1.0f));
   // h = cond_x_merge_linear(x_merged)
   float *cur = m->hA.p, *oth = m->hB.p;
   CK(cfm_bias_rows(cur, d, m->merge_b, R, d, s));
-  BL(gemm(bl, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 1.0f));
+  CK(gemm(s, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 1.0f));
   // U-ViT blocks with long skips (cfm.rs:553-563)
   int nsk = 0;
   for (int i = 0; i < Lc; i++) {
@@ -235,31 +211,31 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     if (i > split && nsk > 0) {  // skip_in_linear([h, skip]) as two accumulating GEMMs
       const float *sk = m->skips[--nsk].p;
       CK(cfm_bias_rows(oth, d, b.skip_b, R, d, s));
-      BL(gemm(bl, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 1.0f));
-      BL(gemm(bl, R, d, d, sk, d, b.skip_w + d, 2 * d, oth, d, 1.0f));
+      CK(gemm(s, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 1.0f));
+      CK(gemm(s, R, d, d, sk, d, b.skip_w + d, 2 * d, oth, d, 1.0f));
       xin = oth;
       oth = cur;
       cur = xin;
     }
     const float *mod_a = m->mods.p + (size_t)(2 * i) * 2 * d, *mod_f = m->mods.p + (size_t)(2 * i + 1) * 2 * d;
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_a, na2, b.an_w, s));
-    BL(gemm(bl, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
+    CK(gemm(s, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
     CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p,
                      reinterpret_cast<uint16_t *>(m->kvs.p), s));
-    BL(gemm(bl, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
+    CK(gemm(s, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
-    BL(gemm(bl, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
+    CK(gemm(s, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
     CK(cfm_swiglu(m->gu.p, R, F, m->act.p, s));
-    BL(gemm(bl, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
+    CK(gemm(s, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
     if (i < split) CK(hipMemcpyAsync(m->skips[nsk++].p, xin, sizeof(float) * R * d, hipMemcpyDeviceToDevice, s));
   }
   // transformer.norm, x_res = skip_linear([h, x_t]), h = conv1(x_res)
   CK(cfm_adaln(cur, m->n.p, R, T, d, m->mods.p + (size_t)(2 * Lc) * 2 * d, na2, m->tn_w, s));
   CK(cfm_bias_rows(m->xres.p, d, m->skl_b, R, d, s));
-  BL(gemm(bl, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 1.0f));
-  BL(gemm(bl, R, d, C, x_t, C, m->skl_w + d, d + C, m->xres.p, d, 1.0f));
+  CK(gemm(s, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 1.0f));
+  CK(gemm(s, R, d, C, x_t, C, m->skl_w + d, d + C, m->xres.p, d, 1.0f));
   CK(cfm_bias_rows(oth, d, m->c1_b, R, d, s));
-  BL(gemm(bl, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 1.0f));
+  CK(gemm(s, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 1.0f));
   // WaveNet (cfm.rs:373-408): h in a zero-padded [B][T + 2 pad][d] buffer
   CK(cfm_pad_rows(oth, B, T, d, pad, m->hpad.p, s));
   CK(hipMemsetAsync(m->oacc.p, 0, sizeof(float) * R * d, s));
@@ -268,31 +244,21 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     const WnLayer &w = m->wn[l];
     const bool last = l + 1 == NL;
     const int rso = last ? d : 2 * d;
-    const float one = 1.0f;
-    if (!force_rocblas() && cfm_gemm_fits(m->hpad.p, d, w.in_w, K * d, K * d)) {
-      // all taps as one product: row t of the padded input read K * d wide (rows t .. t+K-1)
-      CK(cfm_gemm(B, T, 2 * d, K * d, m->hpad.p, d, sp, w.in_w, K * d, 0, m->acts.p, 2 * d, (long)T * 2 * d, 0.0f,
-                  s));
-    } else {
-      for (int k = 0; k < K; k++) {  // tap k reads padded rows t + k
-        const float beta = k == 0 ? 0.0f : 1.0f;
-        BL(rocblas_sgemm_strided_batched(bl, rocblas_operation_transpose, rocblas_operation_none, 2 * d, T, d, &one,
-                                         w.in_w + (size_t)k * d, K * d, 0, m->hpad.p + (size_t)k * d, d, sp, &beta,
-                                         m->acts.p, 2 * d, (long)T * 2 * d, B));
-      }
-    }
+    // all taps as one product: row t of the padded input read K * d wide (rows t .. t+K-1);
+    // d is a multiple of 64, so the operands always suit the MFMA GEMM
+    CK(cfm_gemm(B, T, 2 * d, K * d, m->hpad.p, d, sp, w.in_w, K * d, 0, m->acts.p, 2 * d, (long)T * 2 * d, 0.0f, s));
     CK(cfm_gate(m->acts.p, w.in_b, m->wng.p + (size_t)l * 2 * d, 2 * d * NL, R, T, d, m->act.p, s));
-    BL(gemm(bl, R, rso, d, m->act.p, d, w.rs_w, d, m->rs.p, rso, 0.0f));
+    CK(gemm(s, R, rso, d, m->act.p, d, w.rs_w, d, m->rs.p, rso, 0.0f));
     CK(cfm_res_skip(m->rs.p, w.rs_b, last ? 1 : 0, R, T, d, pad, m->hpad.p, m->oacc.p, s));
   }
   // h = wavenet + res_projection(x_res); FinalLayer; conv2
   CK(cfm_add_bias(m->oacc.p, d, m->rp_b, R, d, s));
-  BL(gemm(bl, R, d, d, m->xres.p, d, m->rp_w, d, m->oacc.p, d, 1.0f));
+  CK(gemm(s, R, d, d, m->xres.p, d, m->rp_w, d, m->oacc.p, d, 1.0f));
   CK(cfm_final_norm(m->oacc.p, m->n.p, R, T, d, m->fmod.p, s));
   CK(cfm_bias_rows(cur, d, m->fl_b, R, d, s));
-  BL(gemm(bl, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 1.0f));
+  CK(gemm(s, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 1.0f));
   CK(cfm_bias_rows(m->v.p, C, m->c2_b, R, C, s));
-  BL(gemm(bl, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 1.0f));
+  CK(gemm(s, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 1.0f));
   return ITTS_OK;
 }
 
@@ -394,10 +360,6 @@ itts_status itts_cfm_create(const itts_cfm_config *cfg, const char *const *names
     return st;
   };
   if (hipStreamCreate(&m->s) != hipSuccess) return fail(cerr(ITTS_E_DEVICE, "hipStreamCreate failed"));
-  if (rocblas_create_handle(&m->blas) != rocblas_status_success)
-    return fail(cerr(ITTS_E_DEVICE, "rocblas_create_handle failed"));
-  if (rocblas_set_stream(m->blas, m->s) != rocblas_status_success)
-    return fail(cerr(ITTS_E_DEVICE, "rocblas_set_stream failed"));
   if (hipMalloc(&m->arena, top * sizeof(float)) != hipSuccess)
     return fail(cerr(ITTS_E_DEVICE, "out of device memory for the CFM weights (%zu bytes)", top * sizeof(float)));
   for (const auto &kv : seen) {
@@ -504,7 +466,7 @@ itts_status itts_cfm_solve_euler(itts_cfm *m, const float *cat_condition, int32_
   CK(hipMemsetAsync(m->merged.p, 0, sizeof(float) * 2 * T * MD, s));
   CK(cfm_static_tail(m->merged.p, MD, C, d, S, T, m->refm.p, T_ref, m->sty.p, s));
   CK(cfm_bias_rows(m->merged.p + 2 * C, MD, m->cond_b, 2 * T, d, s));
-  BL(gemm(m->blas, T, d, d, m->catc.p, d, m->cond_w, d, m->merged.p + 2 * C, MD, 1.0f));
+  CK(gemm(m->s, T, d, d, m->catc.p, d, m->cond_w, d, m->merged.p + 2 * C, MD, 1.0f));
   CK(hipEventRecord(m->e0, s));
   const float dt = 1.0f / (float)n_timesteps;
   for (int step = 0; step < n_timesteps; step++) {

@@ -262,6 +262,10 @@ int cfm_kv_split_halves(int B, int T, int H);
 bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K);
 hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
                     float *y, int ldy, long sy, float beta, hipStream_t s);
+// The same product in fp32 FMAs for few rows (any M, any alignment; float4 loads when K,
+// lda, ldw, sa, sw are multiples of 4 and A, W are 16-byte aligned); beta 0 never reads y.
+hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
+                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s);
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
                          float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);

@@ -1,12 +1,14 @@
 // Stage-2 CFM DiT estimator kernels for gfx950 (crates/core/src/models/cfm.rs).
 //
-// The estimator's linears are plain fp32 GEMMs and run in rocBLAS; the kernels here are
-// the parts around them, fused where a GEMM's output is consumed elementwise: the
-// timestep frequency embedding, AdaLN over RMSNorm (one pass per row), non-causal
-// MFMA attention with rope applied while K and Q are staged (no rotated copy in HBM), SwiGLU,
-// WaveNet's gated activation and residual / skip accumulation, the final layer norm with
-// its modulation, and the Euler / classifier-free-guidance update.  Activations are
-// [B][T][C] row-major fp32.
+// The estimator's linears: the split-fp16 MFMA GEMM (fp32 operands split into fp16 hi/lo
+// parts per K tile, fp32 accumulation) for products of 64 rows and more, and a few-row fp32
+// FMA product (one wave per output column) for the per-batch conditioning projections and
+// shorter forwards.  Around them, fused where a GEMM's output is consumed elementwise: the
+// timestep frequency embedding, AdaLN over RMSNorm (one pass per row), non-causal MFMA
+// attention (K with rope applied and V written once per call as fp16 hi/lo planes, Q
+// rotated while staged), SwiGLU, WaveNet's gated activation and residual / skip
+// accumulation, the final layer norm with its modulation, and the Euler /
+// classifier-free-guidance update.  Activations are [B][T][C] row-major fp32.
 #include "kernels.h"
 
 namespace itts {
@@ -628,6 +630,57 @@ __global__ void pad_rows_kernel(const float *x, int B, int T, int d, int pad, fl
   hp[i] = (t >= 0 && t < T) ? x[((size_t)b * T + t) * d + c] : 0.0f;
 }
 
+// Few-row product y[z][m][n] = sum_k A[z][m][k] W[z][n][k] + beta y[z][m][n] in fp32 FMAs:
+// the per-batch timestep / AdaLN / WaveNet-conditioning projections (2 rows, the CFG pair)
+// and forwards of fewer than 64 rows.  One wave per output column n streams W's row n once
+// (coalesced, VEC floats per lane) against MT rows of A (L2-resident); lane partial sums
+// meet in a DPP reduction.  Block: 4 waves = 4 columns; grid (N/4, M/MT, batch).
+template <int MT, int VEC>
+__global__ __launch_bounds__(256) void rows_gemm_kernel(const float *__restrict__ A, int lda, long sa,
+                                                        const float *__restrict__ W, int ldw, long sw, float *y,
+                                                        int ldy, long sy, int M, int N, int K, float beta) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int m0 = blockIdx.y * MT, z = blockIdx.z;
+  const float *w = W + z * sw + (size_t)n * ldw;
+  const float *a[MT];
+#pragma unroll
+  for (int j = 0; j < MT; j++) a[j] = A + z * sa + (size_t)(m0 + j < M ? m0 + j : m0) * lda;
+  float acc[MT];
+#pragma unroll
+  for (int j = 0; j < MT; j++) acc[j] = 0.0f;
+  if constexpr (VEC == 4) {
+    for (int k = 4 * lane; k < K; k += 256) {
+      const float4 wv = *reinterpret_cast<const float4 *>(w + k);
+#pragma unroll
+      for (int j = 0; j < MT; j++) {
+        const float4 av = *reinterpret_cast<const float4 *>(a[j] + k);
+        acc[j] = fmaf(av.x, wv.x, acc[j]);
+        acc[j] = fmaf(av.y, wv.y, acc[j]);
+        acc[j] = fmaf(av.z, wv.z, acc[j]);
+        acc[j] = fmaf(av.w, wv.w, acc[j]);
+      }
+    }
+  } else {
+    for (int k = lane; k < K; k += 64) {
+      const float wv = w[k];
+#pragma unroll
+      for (int j = 0; j < MT; j++) acc[j] = fmaf(a[j][k], wv, acc[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MT; j++) acc[j] = wave64_sum_dpp(acc[j]);
+  if (lane < MT && m0 + lane < M) {
+    float v = acc[0];
+#pragma unroll
+    for (int j = 1; j < MT; j++)
+      if (lane == j) v = acc[j];
+    float *dst = y + z * sy + (size_t)(m0 + lane) * ldy + n;
+    *dst = beta != 0.0f ? v + beta * *dst : v;
+  }
+}
+
 __global__ void fill_kernel(float *p, int n, float v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -709,6 +762,28 @@ hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, lon
   if (batch < 1 || M < 1 || N < 1 || K < 1 || !cfm_gemm_fits(A, lda, W, ldw, K)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_gemm_kernel, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa, W,
                      ldw, sw, y, ldy, sy, M, N, K, beta);
+  return hipGetLastError();
+}
+hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
+                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s) {
+  if (batch < 1 || M < 1 || N < 1 || K < 1 || lda < K || ldw < K || ldy < N) return hipErrorInvalidValue;
+  const bool v4 = K % 4 == 0 && lda % 4 == 0 && ldw % 4 == 0 && sa % 4 == 0 && sw % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0;
+  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const dim3 grid((N + 3) / 4, (M + mt - 1) / mt, batch);
+#define ROWS_GEMM(MT, VEC)                                                                                        hipLaunchKernelGGL((rows_gemm_kernel<MT, VEC>), grid, dim3(256), 0, s, A, lda, sa, W, ldw, sw, y, ldy, sy, M, N,                      K, beta)
+  if (v4) {
+    if (mt == 1) ROWS_GEMM(1, 4);
+    else if (mt == 2) ROWS_GEMM(2, 4);
+    else if (mt == 4) ROWS_GEMM(4, 4);
+    else ROWS_GEMM(8, 4);
+  } else {
+    if (mt == 1) ROWS_GEMM(1, 1);
+    else if (mt == 2) ROWS_GEMM(2, 1);
+    else if (mt == 4) ROWS_GEMM(4, 1);
+    else ROWS_GEMM(8, 1);
+  }
+#undef ROWS_GEMM
   return hipGetLastError();
 }
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s) {

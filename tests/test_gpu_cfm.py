@@ -98,15 +98,42 @@ def test_validation(small):
         CfmDit(wrong, SMALL_CONFIG)
 
 
-def test_full_size_forward_matches_oracle():
-    """The reference's shape (dim 512, 13 layers, 8 heads, WaveNet 8 x kernel 5) at 96 frames."""
-    say("[gpu] full-size CFM forward T=96")
+# dim 256 (the one-wave AdaLN with 4 values per lane), and channel counts that are not
+# multiples of 4: the merge and skip products then take the few-row fp32 product's scalar
+# loads at every row count
+MID_CONFIG = dict(dim=256, n_layers=3, n_heads=4, inter=384, in_ch=18, style_dim=30, wn_layers=2, wn_kernel=3)
+
+
+@pytest.mark.parametrize("T", [7, 100])
+def test_forward_d256_unaligned_channels(T):
+    say(f"[gpu] cfm forward dim 256, in_ch 18, T={T}")
+    W = synth.make_cfm_weights(MID_CONFIG, seed=3)
+    m = CfmDit(W, MID_CONFIG)
+    try:
+        rng = np.random.default_rng(40 + T)
+        C = MID_CONFIG["in_ch"]
+        x_t = rng.standard_normal((2, T, C)).astype(np.float32)
+        x_m = rng.standard_normal((2, T, merged_dim(MID_CONFIG))).astype(np.float32)
+        x_m[..., :C] = x_t
+        t = np.array([0.3, 0.7], np.float32)
+        got = m.forward_merged(x_t, x_m, t)
+        ref = ito.CfmModel(W, MID_CONFIG).forward_merged(x_t, x_m, t)
+        assert got.shape == ref.shape == (2, C, T)
+        assert rel(got, ref) < 2e-4
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("T", [96, 1033])
+def test_full_size_forward_matches_oracle(T):
+    """The reference's shape (dim 512, 13 layers, 8 heads, WaveNet 8 x kernel 5) at 96 frames
+    and at the 1033 frames of the benchmarked solve (10 s of audio)."""
+    say(f"[gpu] full-size CFM forward T={T}")
     W = synth.make_cfm_weights(FULL_CONFIG, seed=11)
     assert set(W) == set(tensor_shapes(FULL_CONFIG))
     m = CfmDit(W, FULL_CONFIG)
     try:
         rng = np.random.default_rng(2)
-        T = 96
         x_t = rng.standard_normal((2, T, 80)).astype(np.float32)
         x_m = rng.standard_normal((2, T, merged_dim(FULL_CONFIG))).astype(np.float32)
         x_m[..., :80] = x_t
