@@ -414,15 +414,22 @@ struct PersistChain {
 };
 PersistChain g_persist_chain[kMaxDevices];
 
-itts_status launch_persist_chained(itts_gpt *g, itts_kv *kv) {
+// Runs launch() (work on g->stream that contains persistent launches) ordered after every
+// earlier persistent launch of another decoder on the device.
+template <class F>
+itts_status persist_chained(itts_gpt *g, F launch) {
   PersistChain &ch = g_persist_chain[g->device];
   std::lock_guard<std::mutex> lock(ch.mu);
   if (!ch.done) HIP_TRY(hipEventCreateWithFlags(&ch.done, hipEventDisableTiming));
   if (ch.last && ch.last != g->stream) HIP_TRY(hipStreamWaitEvent(g->stream, ch.done, 0));
-  HIP_TRY(launch_decode_persist(kv->pa, g->cfg.quant_bits, g->ptype(), g->stream));
+  HIP_TRY(launch());
   HIP_TRY(hipEventRecord(ch.done, g->stream));
   ch.last = g->stream;
   return ITTS_OK;
+}
+
+itts_status launch_persist_chained(itts_gpt *g, itts_kv *kv) {
+  return persist_chained(g, [&] { return launch_decode_persist(kv->pa, g->cfg.quant_bits, g->ptype(), g->stream); });
 }
 
 itts_status enqueue_decode_step(itts_gpt *g, itts_kv *kv) {
@@ -1362,9 +1369,28 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     if (le != hipSuccess) return set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
     return enqueue_decode_step(gpt, kv);
   };
-  // capture one decode iteration (sample, then step) once per cache and parameters
-  // the persistent step is enqueued directly, never captured
-  const bool use_graph = gpt->use_graph && !kv->persist;
+  // Replay in batches of `batch` iterations (sample, then step).  One graph is captured
+  // once per cache and sampling parameters: the whole batch for the persistent step (its
+  // launch is ordered against other decoders' persistent launches around the graph), one
+  // iteration for the multi-kernel step.
+  const int batch = 8;
+  const bool use_graph = gpt->use_graph;
+  const int per_graph = kv->persist ? batch : 1;
+  auto enqueue_captured = [&]() -> itts_status {
+    for (int i = 0; i < per_graph; i++) {
+      hipError_t le = launch_sampler(gpt->logits.as<float>(), c.mel_vocab, nullptr, ds, nullptr, nullptr,
+                                     kv->ctl.as<DecodeCtl>(), kv->codes.as<int32_t>(), c.mel_vocab - 1, 1,
+                                     gpt->stream);
+      if (le != hipSuccess) return set_error(ITTS_E_DEVICE, "sampler launch failed: %s", hipGetErrorName(le));
+      if (kv->persist) {
+        le = launch_decode_persist(kv->pa, c.quant_bits, gpt->ptype(), gpt->stream);
+        if (le != hipSuccess) return set_error(ITTS_E_DEVICE, "decode step launch failed: %s", hipGetErrorName(le));
+      } else if (itts_status st2 = enqueue_decode_step(gpt, kv)) {
+        return st2;
+      }
+    }
+    return ITTS_OK;
+  };
   if (use_graph && (!kv->have_graph || !same_sampling(kv->gkey, ds))) {
     if (kv->gexec) {
       (void)hipGraphExecDestroy(kv->gexec);
@@ -1377,7 +1403,7 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     kv->have_graph = false;
     HIP_TRY(hipStreamSynchronize(gpt->stream));
     HIP_TRY(hipStreamBeginCapture(gpt->stream, hipStreamCaptureModeThreadLocal));
-    itts_status es = enqueue_iteration();
+    itts_status es = enqueue_captured();
     hipGraph_t graph = nullptr;
     hipError_t ce = hipStreamEndCapture(gpt->stream, &graph);
     if (es) {
@@ -1390,9 +1416,8 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     kv->gkey = ds;
     kv->have_graph = true;
   }
-  // Replay in batches, keeping one batch in flight while the previous one's control
-  // block is inspected; iterations after `done` exit at their first instruction.
-  const int batch = 8;
+  // Keep one batch in flight while the previous one's control block is inspected;
+  // iterations after `done` exit at their first instruction.
   DecodeCtl *slot[2] = {kv->host_ctl, kv->host_ctl + 1};
   hipEvent_t ev[2];
   HIP_TRY(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
@@ -1405,12 +1430,17 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     (void)hipEventDestroy(ev[1]);
   };
   auto launch_batch = [&](int which) -> hipError_t {
-    for (int i = 0; i < batch; i++) {
-      if (use_graph) {
-        hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
-        if (e != hipSuccess) return e;
-      } else if (enqueue_iteration() != ITTS_OK) {
+    if (use_graph && kv->persist) {
+      if (persist_chained(gpt, [&] { return hipGraphLaunch(kv->gexec, gpt->stream); }) != ITTS_OK)
         return hipErrorLaunchFailure;
+    } else {
+      for (int i = 0; i < batch; i++) {
+        if (use_graph) {
+          hipError_t e = hipGraphLaunch(kv->gexec, gpt->stream);
+          if (e != hipSuccess) return e;
+        } else if (enqueue_iteration() != ITTS_OK) {
+          return hipErrorLaunchFailure;
+        }
       }
     }
     hipError_t e = hipMemcpyAsync(slot[which], kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost,
