@@ -352,6 +352,11 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     constexpr int TILE = BM * BN;
     uint64_t *wsb = reinterpret_cast<uint64_t *>(a.ws + (size_t)tile * S * TILE);
     uint64_t *mine = wsb + (size_t)t.ks * (TILE / 2);
+    // register pair h of sub-tile i2 holds rows from `dead` on only when every one of its
+    // rows is past M (few-row tiles): those pairs are neither stored nor summed
+    auto dead = [&](int i2, int h) {
+      return m0 + wm * 32 * TM + i2 * 32 + (h >> 1) * 8 + ((2 * h) & 3) >= M;
+    };
     if (worker) {
 #pragma unroll
       for (int i2 = 0; i2 < TM; i2++)
@@ -359,6 +364,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
         for (int j = 0; j < TN; j++)
 #pragma unroll
           for (int h = 0; h < 8; h++) {
+            if (dead(i2, h)) continue;
             const float2 v = make_float2(acc[i2][j][2 * h], acc[i2][j][2 * h + 1]);
             __hip_atomic_store(mine + ((((wave * TM + i2) * TN + j) * 8 + h) * 64 + lane),
                                __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -384,6 +390,11 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
             } else {
 #pragma unroll
               for (int h = 0; h < 8; h++) {
+                if (dead(i2, h)) {
+                  v[2 * h] = 0.0f;
+                  v[2 * h + 1] = 0.0f;
+                  continue;
+                }
                 const float2 w = __builtin_bit_cast(
                     float2, __hip_atomic_load(wsb + (size_t)s2 * (TILE / 2) + base + h * 64, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT));
