@@ -508,6 +508,218 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
   }
 }
 
+// ---- few-row products (M <= 8: the batched decode step) ---------------------------------
+// The 64-row tiles above spend most of a launch filling the ring for a few real rows.  Here
+// a block of four waves takes 64 output columns (two 32-column MFMA tiles) over 4 gw K
+// groups, gw per wave (issued together), with no LDS staging: each lane loads its activation and code
+// fragments straight into registers (a lane's 16 codes of a column are one 16-byte load,
+// its 16 activations of a row two), in the K order the tiles above use.  Rows past M are
+// zero fragments; in the 32 x 32 result a lane's rows 4h .. 4h+3 (h = lane >> 5) are the
+// only live ones.  The four waves' partials are added in wave order in LDS; the K splits
+// (blocks) in split order by the last block of the column tile to arrive, as above.
+constexpr int kFewRows = 8, kFewMaxGw = 2, kFewMaxSplits = 16;
+
+template <int BITS, int PT, int EPI, int KVT>
+__global__ __launch_bounds__(256) void few_kernel(GemmArgs a, int nN, int S, int gw) {
+  __shared__ float red[4][512];
+  __shared__ float gel[kFewRows][65];
+  __shared__ uint32_t last_flag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, c = lane & 31;
+  const int tn = blockIdx.x % nN, ks = blockIdx.x / nN;
+  const int N = a.ql.N, K = a.ql.K, G = K / kGroup, M = a.M;
+  const int n0 = tn * 64;
+  // this wave's groups: ks * 4 gw + 4 i + wave, i < gw (none past G)
+  floatx4 acc[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
+  u32x4 xa[kFewMaxGw][2][2][2];  // [group][plane][kp][half]: row c, K 32 kp + 16 h .. +15
+  u32x4 cq[kFewMaxGw][2][2];     // [group][j][kp] (8-bit: 16 codes; 4-bit: 16 nibbles in .x, .y)
+  float2 sb[kFewMaxGw][2];
+  float gsr[kFewMaxGw][4];       // group sums of the lane's live rows 4h + e
+#pragma unroll
+  for (int gi = 0; gi < kFewMaxGw; gi++) {
+    const int g = ks * 4 * gw + 4 * gi + wave;
+    const bool live = gi < gw && g < G;
+#pragma unroll
+    for (int p2 = 0; p2 < 2; p2++)
+#pragma unroll
+      for (int kp = 0; kp < 2; kp++)
+#pragma unroll
+        for (int q = 0; q < 2; q++) xa[gi][p2][kp][q] = u32x4{0u, 0u, 0u, 0u};
+    if (live && c < M) {
+      const size_t off = (size_t)c * K + (size_t)g * kGroup + 16 * h;
+#pragma unroll
+      for (int kp = 0; kp < 2; kp++) {
+        const u32x4 *ph = reinterpret_cast<const u32x4 *>(a.x.hi + off + 32 * kp);
+        const u32x4 *pl = reinterpret_cast<const u32x4 *>(a.x.lo + off + 32 * kp);
+        xa[gi][0][kp][0] = ph[0];
+        xa[gi][0][kp][1] = ph[1];
+        xa[gi][1][kp][0] = pl[0];
+        xa[gi][1][kp][1] = pl[1];
+      }
+    }
+    // code fragments of columns n0 + 32 j + c (a column past N reads column N - 1, a group
+    // past G reads group 0)
+    const int gl = live ? g : 0;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = min(n0 + 32 * j + c, N - 1);
+#pragma unroll
+      for (int kp = 0; kp < 2; kp++) {
+        if constexpr (BITS == 8) {
+          cq[gi][j][kp] =
+              *reinterpret_cast<const u32x4 *>(a.ql.codes + (size_t)n * K + (size_t)gl * 64 + 32 * kp + 16 * h);
+        } else {
+          const uint2 v =
+              *reinterpret_cast<const uint2 *>(a.ql.codes + (size_t)n * (K / 2) + (size_t)gl * 32 + 16 * kp + 8 * h);
+          cq[gi][j][kp] = u32x4{v.x, v.y, 0u, 0u};
+        }
+      }
+      sb[gi][j] = load_param<PT>(a.ql.params, (size_t)n * G + gl);
+      if constexpr (BITS == 4) sb[gi][j].y = sb[gi][j].y - 16.0f * sb[gi][j].x;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int m = 4 * h + e;
+      gsr[gi][e] = live && m < M ? a.x.gs[(size_t)m * G + g] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int gi = 0; gi < kFewMaxGw; gi++) {
+    if (gi >= gw || ks * 4 * gw + 4 * gi + wave >= G) break;  // wave-uniform
+    floatx16 P[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) P[j][e] = 0.0f;
+#pragma unroll
+    for (int kp = 0; kp < 2; kp++)
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++) {
+        const f16x8 ah = __builtin_bit_cast(f16x8, xa[gi][0][kp][sub]);
+        const f16x8 al = __builtin_bit_cast(f16x8, xa[gi][1][kp][sub]);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          u32x4 b;
+          if constexpr (BITS == 8) {
+            const uint32_t w0 = cq[gi][j][kp][2 * sub], w1 = cq[gi][j][kp][2 * sub + 1];
+            b = u32x4{f16_pair_u8(w0, 0), f16_pair_u8(w0, 16), f16_pair_u8(w1, 0), f16_pair_u8(w1, 16)};
+          } else {
+            const uint32_t w = cq[gi][j][kp][sub];
+            b = u32x4{f16_pair_u4(w, 0), f16_pair_u4(w, 8), f16_pair_u4(w, 16), f16_pair_u4(w, 24)};
+          }
+          const f16x8 bq = __builtin_bit_cast(f16x8, b);
+          P[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bq, P[j], 0, 0, 0);
+          P[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bq, P[j], 0, 0, 0);
+        }
+      }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[j][e] = fmaf(sb[gi][j].x, P[j][e], fmaf(sb[gi][j].y, gsr[gi][e], acc[j][e]));
+  }
+  // the four waves' partials, added in wave order: entry i = (j, e, lane)
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) red[wave][(j * 4 + e) * 64 + lane] = acc[j][e];
+  __syncthreads();
+  float v[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int i = tid + 256 * q;
+    v[q] = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+  }
+  if (S > 1) {
+    // the block's 512 partials at ws[(tile, split)], agent-scope stores (coherent across the
+    // XCDs' L2s); the last block of the tile adds the splits in split order
+    float *wsb = a.ws + (size_t)tn * S * 512;
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+      __hip_atomic_store(wsb + (size_t)ks * 512 + tid + 256 * q, v[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) last_flag = atomicInc(a.cnt + tn, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
+    __syncthreads();
+    if (!last_flag) return;
+    // every split's loads issued before the first add
+    float w[2][kFewMaxSplits];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+      for (int s2 = 0; s2 < kFewMaxSplits; s2++)
+        w[q][s2] = s2 < S && s2 != ks ? __hip_atomic_load(wsb + (size_t)s2 * 512 + tid + 256 * q, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : v[q];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      float t = w[q][0];
+#pragma unroll
+      for (int s2 = 1; s2 < kFewMaxSplits; s2++)
+        if (s2 < S) t += w[q][s2];
+      v[q] = t;
+    }
+  }
+  // entry i -> row m = 4 h + e, column n0 + 32 j + c
+  if constexpr (EPI == kEpiGelu) {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const int i = tid + 256 * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
+      const int m = 4 * (ln >> 5) + e, cl = 32 * j + (ln & 31), n = n0 + cl;
+      const float gv = gelu_tanh(v[q] + a.ql.bias[n]);  // N is a multiple of 64 here
+      gel[m][cl] = gv;
+      if (m < M) {
+        uint32_t hb, lb;
+        split_f16(gv, hb, lb);
+        a.xo.hi[(size_t)m * N + n] = (uint16_t)hb;
+        a.xo.lo[(size_t)m * N + n] = (uint16_t)lb;
+      }
+    }
+    __syncthreads();
+    // per row, the sum of its 64 GELU values in column order (two rows per wave)
+#pragma unroll
+    for (int r2 = 0; r2 < 2; r2++) {
+      const int m = wave + 4 * r2;
+      const float t = wave_sum(gel[m][lane]);
+      if (lane == 0 && m < M) a.xo.gs[(size_t)m * (N / kGroup) + tn] = t;
+    }
+    return;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const int i = tid + 256 * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
+      const int m = 4 * (ln >> 5) + e, n = n0 + 32 * j + (ln & 31);
+      if (m >= M || n >= N) continue;
+      const float val = v[q] + a.ql.bias[n];
+      if constexpr (EPI == kEpiStore) {
+        a.y[(size_t)m * N + n] = val;
+      } else if constexpr (EPI == kEpiResid) {
+        a.y[(size_t)m * N + n] += val;
+      } else {
+        const int d = a.qkv.d_model;
+        if (n < d) {
+          a.qkv.q_out[(size_t)m * d + n] = val;
+        } else {
+          const int idx = n < 2 * d ? n - d : n - 2 * d;
+          const int hh = idx >> 6, e2 = idx & 63;
+          void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
+          int pos = a.qkv.pos0 + m;
+          if (a.qkv.seqs) {  // batched decode: row m is sequence m
+            const BatchSeq &sq = a.qkv.seqs[m];
+            if (sq.ctl->done) continue;
+            pos = sq.ctl->valid_len;
+            cache = static_cast<char *>(n < 2 * d ? sq.k : sq.v) + a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4);
+          }
+          const size_t ci = ((size_t)hh * a.qkv.max_seq + pos) * kHeadDim + e2;
+          if constexpr (KVT == kKvBf16) {
+            static_cast<uint16_t *>(cache)[ci] = (uint16_t)float_to_bf16_bits(val);
+          } else {
+            static_cast<float *>(cache)[ci] = val;
+          }
+        }
+      }
+    }
+  }
+}
+
 // fp32 rows [M][K] -> hi/lo fp16 planes and per-group row sums; one wave per 64-group
 __global__ __launch_bounds__(256) void split_rows_kernel(const float *x, int M, int K, SplitOut o) {
   const int G = K / kGroup;
@@ -661,6 +873,29 @@ hipError_t gemm_dispatch(const GemmArgs &a, const Plan &p, int epi, int kvt, hip
   }
 }
 
+template <int BITS, int PT, int EPI, int KVT>
+hipError_t few_launch(const GemmArgs &a, int nN, int S, int gw, hipStream_t s) {
+  hipLaunchKernelGGL((few_kernel<BITS, PT, EPI, KVT>), dim3(nN * S), dim3(256), 0, s, a, nN, S, gw);
+  return hipGetLastError();
+}
+
+template <int BITS, int PT>
+hipError_t few_dispatch(const GemmArgs &a, int nN, int S, int gw, int epi, int kvt, hipStream_t s) {
+  switch (epi) {
+    case kEpiStore:
+      return few_launch<BITS, PT, kEpiStore, 0>(a, nN, S, gw, s);
+    case kEpiResid:
+      return few_launch<BITS, PT, kEpiResid, 0>(a, nN, S, gw, s);
+    case kEpiGelu:
+      return few_launch<BITS, PT, kEpiGelu, 0>(a, nN, S, gw, s);
+    case kEpiQKV:
+      return kvt == kKvBf16 ? few_launch<BITS, PT, kEpiQKV, kKvBf16>(a, nN, S, gw, s)
+                            : few_launch<BITS, PT, kEpiQKV, kKvF32>(a, nN, S, gw, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 hipError_t gemm_init() {
@@ -679,6 +914,19 @@ size_t gemm_ws_floats(int n_cu) {
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s) {
   if (a.ql.K % kGroup != 0 || a.M <= 0 || a.ql.N <= 0) return hipErrorInvalidValue;
   if (epi == kEpiGelu && a.ql.N % kGroup != 0) return hipErrorInvalidValue;
+  if (a.M <= kFewRows && (bits == 8 || bits == 4)) {
+    // a group per wave while that keeps the splits within kFewMaxSplits, else two
+    const int nN = (a.ql.N + 63) / 64, G = a.ql.K / kGroup;
+    const int gw = (G + 4 * kFewMaxSplits - 1) / (4 * kFewMaxSplits), S = (G + 4 * gw - 1) / (4 * gw);
+    const bool ws_ok = S == 1 || (a.ws && a.cnt && (size_t)nN * S * 512 <= a.ws_floats && nN <= a.cnt_words);
+    if (ws_ok && gw <= kFewMaxGw) {
+      if (bits == 8)
+        return ptype == kParamF16 ? few_dispatch<8, kParamF16>(a, nN, S, gw, epi, kvt, s)
+                                  : few_dispatch<8, kParamF32>(a, nN, S, gw, epi, kvt, s);
+      return ptype == kParamF16 ? few_dispatch<4, kParamF16>(a, nN, S, gw, epi, kvt, s)
+                                : few_dispatch<4, kParamF32>(a, nN, S, gw, epi, kvt, s);
+    }
+  }
   const Plan p = make_plan(a, bits, ptype);
   if (p.S > 1 && (a.ws == nullptr || a.cnt == nullptr)) return hipErrorInvalidValue;
   if (bits == 8) {
