@@ -475,15 +475,39 @@ __global__ __launch_bounds__(256) void attn_decode_batch_kernel(const float *q, 
   auto ld = [&](int i) {
     return __uint_as_float(__hip_atomic_load(ph + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   };
-  float M = -INFINITY;
-  for (int s2 = 0; s2 < S; s2++) M = fmaxf(M, ld(s2 * 66));
-  float den = 0.0f, num = 0.0f;
-  for (int s2 = 0; s2 < S; s2++) {
-    const float m = ld(s2 * 66);
-    if (m == -INFINITY) continue;
-    const float f = __expf(m - M);
-    den += ld(s2 * 66 + 1) * f;
-    num += ld(s2 * 66 + 2 + lane) * f;
+  // every split's (max, denominator, output) loaded before the first use when they fit
+  // kCombineRegs registers each (one round trip), else split by split; same order and
+  // arithmetic either way
+  constexpr int kCombineRegs = 16;
+  float M = -INFINITY, den = 0.0f, num = 0.0f;
+  if (S <= kCombineRegs) {
+    float mv[kCombineRegs], lv[kCombineRegs], ov[kCombineRegs];
+#pragma unroll
+    for (int s2 = 0; s2 < kCombineRegs; s2++)
+      if (s2 < S) {
+        mv[s2] = ld(s2 * 66);
+        lv[s2] = ld(s2 * 66 + 1);
+        ov[s2] = ld(s2 * 66 + 2 + lane);
+      }
+#pragma unroll
+    for (int s2 = 0; s2 < kCombineRegs; s2++)
+      if (s2 < S) M = fmaxf(M, mv[s2]);
+#pragma unroll
+    for (int s2 = 0; s2 < kCombineRegs; s2++)
+      if (s2 < S && mv[s2] != -INFINITY) {
+        const float f = __expf(mv[s2] - M);
+        den += lv[s2] * f;
+        num += ov[s2] * f;
+      }
+  } else {
+    for (int s2 = 0; s2 < S; s2++) M = fmaxf(M, ld(s2 * 66));
+    for (int s2 = 0; s2 < S; s2++) {
+      const float m = ld(s2 * 66);
+      if (m == -INFINITY) continue;
+      const float f = __expf(m - M);
+      den += ld(s2 * 66 + 1) * f;
+      num += ld(s2 * 66 + 2 + lane) * f;
+    }
   }
   const float v = num / den;
   uint32_t hi, lo;

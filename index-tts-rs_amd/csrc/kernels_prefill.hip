@@ -18,6 +18,8 @@
 // Small M is spread over the chip by splitting K: each split stores its partial tile,
 // and the last split to arrive at a tile (wrapping counter) adds the partials in split
 // order, so the result does not depend on arrival order.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace itts {
@@ -532,7 +534,10 @@ __global__ __launch_bounds__(256) void few_kernel(GemmArgs a, int nN, int S, int
   floatx4 acc[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
   u32x4 xa[kFewMaxGw][2][2][2];  // [group][plane][kp][half]: row c, K 32 kp + 16 h .. +15
   u32x4 cq[kFewMaxGw][2][2];     // [group][j][kp] (8-bit: 16 codes; 4-bit: 16 nibbles in .x, .y)
-  float2 sb[kFewMaxGw][2];
+  // parameters stay raw until the products (converting them here would wait for each
+  // group's loads in turn)
+  using PRaw = typename std::conditional<PT == kParamF16, uint32_t, float2>::type;
+  PRaw pr[kFewMaxGw][2];
   float gsr[kFewMaxGw][4];       // group sums of the lane's live rows 4h + e
 #pragma unroll
   for (int gi = 0; gi < kFewMaxGw; gi++) {
@@ -573,8 +578,7 @@ __global__ __launch_bounds__(256) void few_kernel(GemmArgs a, int nN, int S, int
           cq[gi][j][kp] = u32x4{v.x, v.y, 0u, 0u};
         }
       }
-      sb[gi][j] = load_param<PT>(a.ql.params, (size_t)n * G + gl);
-      if constexpr (BITS == 4) sb[gi][j].y = sb[gi][j].y - 16.0f * sb[gi][j].x;
+      pr[gi][j] = static_cast<const PRaw *>(a.ql.params)[(size_t)n * G + gl];
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -612,9 +616,16 @@ __global__ __launch_bounds__(256) void few_kernel(GemmArgs a, int nN, int S, int
         }
       }
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < 2; j++) {
+      float2 sb;
+      if constexpr (PT == kParamF16)
+        sb = make_float2(half_bits_to_float(pr[gi][j] & 0xffffu), half_bits_to_float(pr[gi][j] >> 16));
+      else
+        sb = pr[gi][j];
+      if constexpr (BITS == 4) sb.y = sb.y - 16.0f * sb.x;
 #pragma unroll
-      for (int e = 0; e < 4; e++) acc[j][e] = fmaf(sb[gi][j].x, P[j][e], fmaf(sb[gi][j].y, gsr[gi][e], acc[j][e]));
+      for (int e = 0; e < 4; e++) acc[j][e] = fmaf(sb.x, P[j][e], fmaf(sb.y, gsr[gi][e], acc[j][e]));
+    }
   }
   // the four waves' partials, added in wave order: entry i = (j, e, lane)
 #pragma unroll
