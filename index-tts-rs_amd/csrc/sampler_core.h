@@ -93,21 +93,32 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = (n + kSampThreads - 1) / kSampThreads;
   const int i0 = tid * E;
-  // (1) load, STOP mask, repetition penalty (x<0 ? x*p : x/p)
+  // (1) load, STOP mask, repetition penalty (x<0 ? x*p : x/p).  Every load is issued before
+  // the first store (penalised_out may be src), and the thread's E <= 9 consecutive ids
+  // span at most two seen words, read once.
   float v[kSampPerThread];
+#pragma unroll
+  for (int e = 0; e < kSampPerThread; e++) v[e] = e < E && i0 + e < n ? src[i0 + e] : 0.0f;
+  const int w0 = i0 >> 6;
+  const uint64_t sw0 = p.apply_penalty && w0 < kSeenWords ? seen[w0] : 0ull;
+  const uint64_t sw1 = p.apply_penalty && w0 + 1 < kSeenWords ? seen[w0 + 1] : 0ull;
 #pragma unroll
   for (int e = 0; e < kSampPerThread; e++) {
     const int i = i0 + e;
-    float x = 0.0f;
     if (e < E && i < n) {
-      x = src[i];
+      float x = v[e];
       if (mask_stop && i == stop_tok) x = -INFINITY;
-      if (p.apply_penalty && (i >> 6) < kSeenWords && ((seen[i >> 6] >> (i & 63)) & 1ull)) {
+      const uint64_t sw = (i >> 6) == w0 ? sw0 : sw1;
+      if (p.apply_penalty && (i >> 6) < kSeenWords && ((sw >> (i & 63)) & 1ull)) {
         x = x < 0.0f ? mul_rn(x, p.penalty) : div_rn(x, p.penalty);
       }
-      if (penalised_out) penalised_out[i] = x;
+      v[e] = x;
     }
-    v[e] = x;
+  }
+  if (penalised_out) {
+#pragma unroll
+    for (int e = 0; e < kSampPerThread; e++)
+      if (e < E && i0 + e < n) penalised_out[i0 + e] = v[e];
   }
 
   int32_t result = 0;
