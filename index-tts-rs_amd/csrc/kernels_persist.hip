@@ -270,14 +270,18 @@ __device__ inline float2 dot32(const u32x4 c, const float *xc) {
   for (int i = 0; i < 4; i++) {
     const float4 xa = *reinterpret_cast<const float4 *>(xc + 8 * i);
     const float4 xb = *reinterpret_cast<const float4 *>(xc + 8 * i + 4);
-    acc += xa.x * (float)(w[i] & 0xfu);
-    acc += xa.y * (float)((w[i] >> 4) & 0xfu);
-    acc += xa.z * (float)((w[i] >> 8) & 0xfu);
-    acc += xa.w * (float)((w[i] >> 12) & 0xfu);
-    acc += xb.x * (float)((w[i] >> 16) & 0xfu);
-    acc += xb.y * (float)((w[i] >> 20) & 0xfu);
-    acc += xb.z * (float)((w[i] >> 24) & 0xfu);
-    acc += xb.w * (float)(w[i] >> 28);
+    // even and odd nibbles as bytes, so that each code converts with one byte-select
+    // conversion (the same values, summed in the same order)
+    uint32_t lo = w[i] & 0x0f0f0f0fu, hi = (w[i] >> 4) & 0x0f0f0f0fu;
+    asm("" : "+v"(lo), "+v"(hi));  // opaque: otherwise folded back into one bit-field extract per code
+    acc += xa.x * (float)(lo & 0xffu);
+    acc += xa.y * (float)(hi & 0xffu);
+    acc += xa.z * (float)((lo >> 8) & 0xffu);
+    acc += xa.w * (float)((hi >> 8) & 0xffu);
+    acc += xb.x * (float)((lo >> 16) & 0xffu);
+    acc += xb.y * (float)((hi >> 16) & 0xffu);
+    acc += xb.z * (float)(lo >> 24);
+    acc += xb.w * (float)(hi >> 24);
     xs += ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
   }
   return make_float2(acc, xs);
