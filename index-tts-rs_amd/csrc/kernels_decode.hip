@@ -534,61 +534,99 @@ __global__ void advance_batch_kernel(const BatchSeq *seqs, int B) {
   if (b < B && !seqs[b].ctl->done) seqs[b].ctl->valid_len += 1;
 }
 
-// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows).  Scores:
-// lane = key of the 64-key tile.  Values: lane = (key group kg = lane / 8, dims 8 (lane % 8)
-// .. +7); a lane accumulates keys kg, kg + 8, .. of every tile with one 16-byte load each,
-// and the eight key groups are added once at the end.  o returns dimension `lane`.
+// Eight consecutive elements of a cache row, held in the cache dtype until used.
+template <int KVT>
+struct Row8 {
+  uint32_t w[KVT == kKvBf16 ? 4 : 8];
+  __device__ __forceinline__ void load(const void *base, size_t row, int c0) {
+    if constexpr (KVT == kKvBf16) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
+      w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+    } else {
+      const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + row * 64 + c0);
+      const uint4 u0 = p[0], u1 = p[1];
+      w[0] = u0.x; w[1] = u0.y; w[2] = u0.z; w[3] = u0.w;
+      w[4] = u1.x; w[5] = u1.y; w[6] = u1.z; w[7] = u1.w;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < (KVT == kKvBf16 ? 4 : 8); i++) w[i] = 0u;
+  }
+  __device__ __forceinline__ float at(int e) const {
+    if constexpr (KVT == kKvBf16) return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+    return __uint_as_float(w[e]);
+  }
+};
+
+// Score (q.k / 8) of key row `kr`, whose dims 8 dc .. 8 dc + 7 this lane holds against
+// q's in qa, qb: the lane's partial dot, summed over the key's eight lanes (xor 1, xor 2,
+// then the 8-lane mirror; both lanes of each pair form the same sum, so all eight lanes
+// hold one bit-identical score).  Every lane of the wave must be active.
+template <int KVT>
+__device__ __forceinline__ float row_score(const float4 &qa, const float4 &qb, const Row8<KVT> &kr) {
+  float t = qa.x * kr.at(0) + qa.y * kr.at(1) + qa.z * kr.at(2) + qa.w * kr.at(3) +
+            (qb.x * kr.at(4) + qb.y * kr.at(5) + qb.z * kr.at(6) + qb.w * kr.at(7));
+  t += dpp_pair<0xB1>(t);
+  t += dpp_pair<0x4E>(t);
+  t += dpp_pair<0x141>(t);
+  return t * 0.125f;
+}
+
+// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows), 64 keys
+// a tile.  Lane = (key group kg = lane / 8, dims 8 (lane % 8) .. +7): a lane holds keys
+// kg, kg + 8, .. of the tile, K and V rows both spread over eight adjacent lanes (16 bytes
+// each, so a load instruction reads eight whole rows) and all of a tile's loads are in
+// flight at once; probabilities stay in the lane that holds the key, and the eight key
+// groups are added once at the end.  o returns dimension `lane`.
 template <int KVT>
 __device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
-                                  float &m, float &l, float &o, float *p_lds) {
+                                  float &m, float &l, float &o) {
   const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
-  float qr[64];
-#pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const float4 v = reinterpret_cast<const float4 *>(q)[i];
-    qr[4 * i] = v.x;
-    qr[4 * i + 1] = v.y;
-    qr[4 * i + 2] = v.z;
-    qr[4 * i + 3] = v.w;
-  }
+  const float4 qa = reinterpret_cast<const float4 *>(q)[2 * dc], qb = reinterpret_cast<const float4 *>(q)[2 * dc + 1];
   m = -INFINITY;
   l = 0.0f;
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) acc[e] = 0.0f;
   for (int t0 = j0; t0 < j1; t0 += 64) {
-    const int j = t0 + lane;
-    float sc = -INFINITY;
-    if (j < j1) {
-      float kr[64];
-      load_row64<KVT>(kh, (size_t)j, kr);
-      float dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 64; e++) dot += qr[e] * kr[e];
-      sc = dot * 0.125f;
-    }
-    const float mt = wave64_max_dpp(sc);
-    const float mn = fmaxf(m, mt);
-    const float p = (j < j1) ? __expf(sc - mn) : 0.0f;
-    const float corr = (m == -INFINITY) ? 0.0f : __expf(m - mn);
-    l = l * corr + wave64_sum_dpp(p);
-    p_lds[lane] = p;
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] *= corr;
-    const int cnt = min(64, j1 - t0);
+    Row8<KVT> kr[8], vr[8];
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
-      const int kk = kg + 8 * jj;
-      if (kk < cnt) {
-        float v[8];
-        load_row8<KVT>(vh, (size_t)(t0 + kk), dc * 8, v);
-        const float pk = p_lds[kk];
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] += pk * v[e];
+      const int key = t0 + kg + 8 * jj;
+      if (key < j1) {
+        kr[jj].load(kh, (size_t)key, dc * 8);
+        vr[jj].load(vh, (size_t)key, dc * 8);
+      } else {
+        kr[jj].zero();
+        vr[jj].zero();
       }
     }
-    __syncthreads();
+    float sc[8], mt = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const float v = row_score<KVT>(qa, qb, kr[jj]);
+      sc[jj] = t0 + kg + 8 * jj < j1 ? v : -INFINITY;
+      mt = fmaxf(mt, sc[jj]);
+    }
+    mt = wave64_max_dpp(mt);
+    const float mn = fmaxf(m, mt);
+    const float corr = (m == -INFINITY) ? 0.0f : __expf(m - mn);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] *= corr;
+    float ps = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const float p = t0 + kg + 8 * jj < j1 ? __expf(sc[jj] - mn) : 0.0f;
+      ps += p;
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] += p * vr[jj].at(e);
+    }
+    // the tile's probability sum over the eight key groups (lane ^ 8, ^ 16, ^ 32)
+    ps += dpp_pair<0x128>(ps);
+    ps += swizzle_xor16(ps);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * corr + ps;
     m = mn;
   }
   // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits in
@@ -622,12 +660,11 @@ template <int KVT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
                                                           const void *vc, int max_seq, int d,
                                                           SplitOut out) {
-  __shared__ float p_lds[64];
   const int h = blockIdx.x, t = blockIdx.y;
   const size_t hb = (size_t)h * max_seq * 64;
   float m, l, o;
   attn_range<KVT>(q + (size_t)t * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), 0, base + t + 1,
-                  m, l, o, p_lds);
+                  m, l, o);
   // one head is one 64-column group of the c_proj input
   put_split(out, (size_t)t * d + h * 64 + threadIdx.x, (size_t)t * (d / 64) + h, o / l);
 }
@@ -639,28 +676,35 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int ba
 template <int KVT>
 __global__ __launch_bounds__(64) void attn_probe_kernel(const float *q, const void *kc, const void *vc, int ld,
                                                         const int *kstart, int d, AttnProbe pr) {
-  __shared__ float p_lds[64];
-  const int h = pr.head, t = pr.q0 + blockIdx.x, lane = threadIdx.x;
+  const int h = pr.head, t = pr.q0 + blockIdx.x, lane = threadIdx.x, kg = lane >> 3, dc = lane & 7;
   const size_t hb = (size_t)h * ld * 64;
   const int j0 = kstart[t];
   const void *kh = head_base<KVT>(kc, hb);
   const float *qt = q + (size_t)t * d + h * 64;
   float m, l, o;
-  attn_range<KVT>(qt, kh, head_base<KVT>(vc, hb), j0, t + 1, m, l, o, p_lds);
+  attn_range<KVT>(qt, kh, head_base<KVT>(vc, hb), j0, t + 1, m, l, o);
+  const float4 qa = reinterpret_cast<const float4 *>(qt)[2 * dc], qb = reinterpret_cast<const float4 *>(qt)[2 * dc + 1];
   const int w = pr.k1 - pr.k0;
   for (int c0 = 0; c0 < w; c0 += 64) {
+    // the scores of columns c0 + kg + 8 jj exactly as attn_range formed them, then column
+    // c0 + lane taken from lane 8 (lane % 8), element lane / 8
+    Row8<KVT> kr[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int j = pr.k0 + c0 + kg + 8 * jj;
+      if (j >= j0 && j <= t) kr[jj].load(kh, (size_t)j, dc * 8);
+      else kr[jj].zero();
+    }
+    float p = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const float sj = row_score<KVT>(qa, qb, kr[jj]);
+      const float x = __shfl(sj, (lane & 7) << 3, 64);
+      if ((lane >> 3) == jj) p = x;
+    }
     const int c = c0 + lane, j = pr.k0 + c;
     if (c >= w) continue;
-    float p = 0.0f;
-    if (j >= j0 && j <= t) {  // the score exactly as attn_range formed it
-      float kr[64];
-      load_row64<KVT>(kh, (size_t)j, kr);
-      float dot = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 64; e++) dot += qt[e] * kr[e];
-      p = __expf(dot * 0.125f - m) / l;
-    }
-    pr.out[(size_t)(t - pr.q0) * w + c] = p;
+    pr.out[(size_t)(t - pr.q0) * w + c] = (j >= j0 && j <= t) ? __expf(p - m) / l : 0.0f;
   }
 }
 
