@@ -660,7 +660,9 @@ template <int KVT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
                                                           const void *vc, int max_seq, int d,
                                                           SplitOut out) {
-  const int h = blockIdx.x, t = blockIdx.y;
+  // rows in reverse order, so the longest key ranges are dispatched first and the short
+  // ones fill in behind them
+  const int h = blockIdx.x, t = gridDim.y - 1 - blockIdx.y;
   const size_t hb = (size_t)h * max_seq * 64;
   float m, l, o;
   attn_range<KVT>(q + (size_t)t * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), 0, base + t + 1,
