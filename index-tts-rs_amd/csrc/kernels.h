@@ -130,11 +130,13 @@ hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, 
 // K/V [n_head][ld][64] (bf16 or fp32) and attends to keys ks(t)..base + t, ks(t) =
 // kstart[t] or 0; output rows in the GEMM's split form.
 // With kv_split (attn_kv_split_halves(n_head, base + T) 16-bit values), K and V are split into
-// fp16 hi/lo planes once per call instead of once per query tile.
+// fp16 hi/lo planes once per call instead of once per query tile.  With tile_order (a
+// permutation of the ceil(T / 64) query tiles), grid row y runs query tile tile_order[y]:
+// callers list the tiles with the most keys first so the short ones fill in behind them.
 size_t attn_kv_split_halves(int n_head, int keys);
 hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart, const void *kc, const void *vc,
                              int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s,
-                             uint16_t *kv_split = nullptr);
+                             uint16_t *kv_split = nullptr, const int *tile_order = nullptr);
 // out[r] = log_softmax(logits[r])[codes[r]] for R rows of V logits.
 hipError_t launch_log_softmax_pick(const float *logits, int R, int V, const int *codes, float *out, hipStream_t s);
 

@@ -118,9 +118,9 @@ __global__ __launch_bounds__(256) void kv_split_kernel(const void *kc, const voi
 template <int KVT, bool PRE>
 __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, const void *kc, const void *vc,
                                                          int ld, int base, int T, const int *kstart, SplitOut out,
-                                                         const uint16_t *kvs, int Lp) {
+                                                         const uint16_t *kvs, int Lp, const int *order) {
   __shared__ FlashLds sh;
-  const int h = blockIdx.x, q0 = blockIdx.y * kFQ;
+  const int h = blockIdx.x, q0 = (order ? order[blockIdx.y] : (int)blockIdx.y) * kFQ;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const size_t hb = (size_t)h * ld * 64;
   const void *kh = KVT == kKvBf16 ? (const void *)(static_cast<const uint16_t *>(kc) + hb)
@@ -329,7 +329,8 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
 size_t attn_kv_split_halves(int n_head, int keys) { return (size_t)n_head * ((keys + kFK - 1) / kFK) * kFK * 64 * 4; }
 
 hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart, const void *kc, const void *vc,
-                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s, uint16_t *kv_split) {
+                             int ld, int n_head, const SplitOut &out, int kvt, hipStream_t s, uint16_t *kv_split,
+                             const int *tile_order) {
   if (T <= 0 || base + T > ld) return hipErrorInvalidValue;
   dim3 grid(n_head, (T + kFQ - 1) / kFQ);
   const int d = n_head * 64;
@@ -341,20 +342,20 @@ hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart,
     if (kvt == kKvBf16) {
       hipLaunchKernelGGL(kv_split_kernel<kKvBf16>, sg, dim3(256), 0, s, kc, vc, ld, n_head, L, Lp, kv_split);
       hipLaunchKernelGGL((attn_flash_kernel<kKvBf16, true>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
-                         out, kv_split, Lp);
+                         out, kv_split, Lp, tile_order);
     } else {
       hipLaunchKernelGGL(kv_split_kernel<kKvF32>, sg, dim3(256), 0, s, kc, vc, ld, n_head, L, Lp, kv_split);
       hipLaunchKernelGGL((attn_flash_kernel<kKvF32, true>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
-                         out, kv_split, Lp);
+                         out, kv_split, Lp, tile_order);
     }
     return hipGetLastError();
   }
   if (kvt == kKvBf16) {
     hipLaunchKernelGGL((attn_flash_kernel<kKvBf16, false>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
-                       out, nullptr, 0);
+                       out, nullptr, 0, tile_order);
   } else {
     hipLaunchKernelGGL((attn_flash_kernel<kKvF32, false>), grid, dim3(128), 0, s, q, d, kc, vc, ld, base, T, kstart,
-                       out, nullptr, 0);
+                       out, nullptr, 0, tile_order);
   }
   return hipGetLastError();
 }

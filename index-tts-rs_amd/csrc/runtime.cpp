@@ -557,8 +557,19 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
   HIP_TRY(g->rk.ensure(sizeof(float) * (size_t)M * d));
   HIP_TRY(g->pkvs.ensure(sizeof(uint16_t) * attn_kv_split_halves(c.n_head, M)));
   HIP_TRY(g->rv.ensure(sizeof(float) * (size_t)M * d));
-  HIP_TRY(g->kstart.ensure(sizeof(int) * (size_t)M));
-  HIP_TRY(hipMemcpyAsync(g->kstart.p, kstart.data(), sizeof(int) * M, hipMemcpyHostToDevice, s));
+  // kstart, then the attention's query tiles (64 rows) ordered by their key count, most first
+  const int n_tiles = (M + 63) / 64;
+  std::vector<int> ks_order(kstart);
+  ks_order.resize((size_t)M + n_tiles);
+  {
+    std::vector<int> keys(n_tiles);
+    for (int i = 0; i < n_tiles; i++) keys[i] = std::min(M - 1, 64 * i + 63) - kstart[64 * i] + 1;
+    int *order = ks_order.data() + M;
+    for (int i = 0; i < n_tiles; i++) order[i] = i;
+    std::stable_sort(order, order + n_tiles, [&](int a, int b) { return keys[a] > keys[b]; });
+  }
+  HIP_TRY(g->kstart.ensure(sizeof(int) * ks_order.size()));
+  HIP_TRY(hipMemcpyAsync(g->kstart.p, ks_order.data(), sizeof(int) * ks_order.size(), hipMemcpyHostToDevice, s));
   float *X = g->px.as<float>(), *Q = g->pq.as<float>();
   for (int l = 0; l < n_layers; l++) {
     const DevLayer &L = g->layers[l];
@@ -571,7 +582,7 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
         HIP_TRY(launch_attn_probe(Q, M, g->kstart.as<int>(), g->rk.p, g->rv.p, c.n_head,
                                   AttnProbe{p.head, p.q0, p.k0, p.k1, p.out}, kKvF32, s));
     HIP_TRY(launch_attn_flash(Q, M, 0, g->kstart.as<int>(), g->rk.p, g->rv.p, M, c.n_head, g->pa.out(), kKvF32, s,
-                              g->pkvs.as<uint16_t>()));
+                              g->pkvs.as<uint16_t>(), g->kstart.as<int>() + M));
     ga = gemm_args(g, L.proj, g->pa.act(), M);
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
