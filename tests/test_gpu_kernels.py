@@ -66,11 +66,13 @@ def test_gemv_vs_fp64(gpt, bits, pd, N, K):
 
 # Shapes cover: the few-row kernel (M <= 8: one K split, several, a ragged last column
 # tile), the 64 x 64 tile with and without split-K, ragged N and M, the 128 x 128 tile
-# (M > 512) with and without split-K, and the head's N = 8194.
+# (M > 512) with and without split-K, the head's N = 8194, and the 4 x 547-row QKV product
+# (540 tiles, a ragged last M tile of 12 rows).
 @pytest.mark.parametrize("bits,pd", [(8, H.ITTS_F16), (4, H.ITTS_F16), (8, H.ITTS_F32), (4, H.ITTS_F32)])
 @pytest.mark.parametrize("M,N,K", [(2, 37, 192), (8, 3840, 1280), (5, 1280, 5120), (7, 8194, 1280), (3, 96, 128),
                                    (99, 3840, 1280), (130, 1280, 5120), (64, 8194, 1280),
-                                   (235, 1280, 1280), (600, 1280, 1280), (700, 384, 5120)])
+                                   (235, 1280, 1280), (600, 1280, 1280), (700, 384, 5120),
+                                   (2188, 3840, 1280)])
 def test_mfma_gemm_vs_fp64(gpt, bits, pd, M, N, K):
     say(f"[gpu] gemm bits={bits} pd={pd} M={M} N={N} K={K}")
     rng = np.random.default_rng(M + N + K)
