@@ -104,6 +104,7 @@ struct itts_cfm {
   Buf emb, th, t1, t2, st, mods, wng, fmod, tdev;
   Buf hA, hB, n, qkv, att, gu, act, xres, hpad, acts, rs, oacc, v, rope, apo, aml, kvs;
   int rope_T = 0;  // sequence length the rope table holds
+  int n_cu = 0;    // compute units of the device (the attention's split planner)
   std::vector<Buf> skips;
   // solve / API staging
   Buf x, xt, merged, catc, refm, sty, io_a, io_b;
@@ -154,7 +155,7 @@ itts_status ensure_rows(itts_cfm *m, int B, int T) {
   CK(m->v.ensure(R * c.in_ch));
   for (auto &b : m->skips) CK(b.ensure(R * d));
   CK(m->kvs.ensure(((size_t)cfm_kv_split_halves(B, T, c.n_heads) + 1) / 2));  // 16-bit values, float units
-  const size_t S = (size_t)cfm_attn_splits(B, T, c.n_heads);
+  const size_t S = (size_t)cfm_attn_splits(B, T, c.n_heads, m->n_cu);
   if (S > 1) {
     CK(m->apo.ensure(S * R * d));
     CK(m->aml.ensure(S * R * c.n_heads * 2));
@@ -221,7 +222,7 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_a, na2, b.an_w, s));
     CK(gemm(s, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
     CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p,
-                     reinterpret_cast<uint16_t *>(m->kvs.p), s));
+                     reinterpret_cast<uint16_t *>(m->kvs.p), m->n_cu, s));
     CK(gemm(s, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
     CK(gemm(s, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
@@ -360,6 +361,12 @@ itts_status itts_cfm_create(const itts_cfm_config *cfg, const char *const *names
     return st;
   };
   if (hipStreamCreate(&m->s) != hipSuccess) return fail(cerr(ITTS_E_DEVICE, "hipStreamCreate failed"));
+  {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&m->n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return fail(cerr(ITTS_E_DEVICE, "querying the device's compute units failed"));
+  }
   if (hipMalloc(&m->arena, top * sizeof(float)) != hipSuccess)
     return fail(cerr(ITTS_E_DEVICE, "out of device memory for the CFM weights (%zu bytes)", top * sizeof(float)));
   for (const auto &kv : seen) {

@@ -251,9 +251,9 @@ hipError_t cfm_adaln(const float *x, float *y, int R, int T, int d, const float 
 hipError_t cfm_final_norm(const float *x, float *y, int R, int T, int d, const float *mod, hipStream_t s);
 // rope (cos, sin) table [T][32][2] for positions 0..T-1
 hipError_t cfm_rope_table(int T, float *tab, hipStream_t s);
-// Key splits the attention uses for this shape (1..8); with more than one, part_o holds
-// [S][B][T][d] and part_ml [S][B][H][T][2] floats.
-int cfm_attn_splits(int B, int T, int H);
+// Key splits the attention uses for this shape on n_cu compute units (1..8); with more than
+// one, part_o holds [S][B][T][d] and part_ml [S][B][H][T][2] floats.
+int cfm_attn_splits(int B, int T, int H, int n_cu);
 // kv_split: workspace of cfm_kv_split_halves(B, T, H) 16-bit values (K with rope and V as
 // fp16 hi/lo planes, built once per call and shared by every query tile).
 int cfm_kv_split_halves(int B, int T, int H);
@@ -269,7 +269,7 @@ hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, lon
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
                          long sw, float *y, int ldy, long sy, float beta, hipStream_t s);
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
-                         float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s);
+                         float *part_o, float *part_ml, uint16_t *kv_split, int n_cu, hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);
 hipError_t cfm_gate(const float *acts, const float *in_b, const float *g, int ld_g, int R, int T, int d, float *act,
                     hipStream_t s);

@@ -727,20 +727,32 @@ hipError_t cfm_rope_table(int T, float *tab, hipStream_t s) {
                      reinterpret_cast<float2 *>(tab));
   return hipGetLastError();
 }
-int cfm_attn_splits(int B, int T, int H) {
+int cfm_attn_splits(int B, int T, int H, int n_cu) {
+  // The split with the fewest key tiles along the slowest block: rounds of blocks (three
+  // resident per CU: 48 KB of LDS each) x key tiles per split, plus ~1.5 tiles' worth for
+  // the combine pass when split.  (4 splits at 2 x 1033 rows: 1,088 blocks in two rounds of
+  // 5 tiles; 5 splits: 1,360 blocks in two rounds of 4.)
   const int tiles = (T + kAk - 1) / kAk, blocks = H * ((T + kAq - 1) / kAq) * B;
-  int S = (1024 + blocks - 1) / blocks;  // about four blocks of two waves per compute unit
-  S = S < 1 ? 1 : S > 8 ? 8 : S;
-  if (S > tiles) S = tiles;
-  const int kts = (tiles + S - 1) / S;
-  return (tiles + kts - 1) / kts;  // no split without keys
+  const int slots = 3 * (n_cu > 0 ? n_cu : 1);
+  int bestS = 1;
+  double best = 1e30;
+  for (int S0 = 1; S0 <= 8 && S0 <= tiles; S0++) {
+    const int kts = (tiles + S0 - 1) / S0, S = (tiles + kts - 1) / kts;  // no split without keys
+    const int rounds = (blocks * S + slots - 1) / slots;
+    const double cost = (double)rounds * kts + (S > 1 ? 1.5 : 0.0);
+    if (cost < best) {
+      best = cost;
+      bestS = S;
+    }
+  }
+  return bestS;
 }
 int cfm_kv_split_halves(int B, int T, int H) { return B * H * ((T + kAk - 1) / kAk) * kAk * kHd * 4; }
 
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
-                         float *part_o, float *part_ml, uint16_t *kv_split, hipStream_t s) {
+                         float *part_o, float *part_ml, uint16_t *kv_split, int n_cu, hipStream_t s) {
   if (d != H * kHd || T < 1 || !kv_split) return hipErrorInvalidValue;
-  const int S = cfm_attn_splits(B, T, H), tiles = (T + kAk - 1) / kAk, kts = (tiles + S - 1) / S;
+  const int S = cfm_attn_splits(B, T, H, n_cu), tiles = (T + kAk - 1) / kAk, kts = (tiles + S - 1) / S;
   if (S > 1 && (!part_o || !part_ml)) return hipErrorInvalidValue;
   const int Tp = tiles * kAk;
   const long nthreads = (long)B * H * Tp * 8 + (long)B * H * (Tp / 8) * kHd;
