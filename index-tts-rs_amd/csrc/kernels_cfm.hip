@@ -408,20 +408,35 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
 }
 
 // Combines the key splits of cfm_attn_kernel: out = sum_s e^{m_s - M} O_s / sum_s e^{m_s - M} l_s.
+// Every split's (m, l, O) is loaded before the first use (S <= kMaxSplits), so the loads
+// take one round trip; the arithmetic and its order are those of a plain loop over s.
 __global__ void attn_combine_kernel(const float *part_o, const float *part_ml, int S, int B, int T, int d,
                                     float *out) {
+  constexpr int kMaxSplits = 8;  // cfm_attn_splits never returns more
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long)B * T * d) return;
   const int c = (int)(i % d), bt = (int)(i / d), b = bt / T, t = bt % T, h = c / kHd, H = d / kHd;
+  float mv[kMaxSplits], lv[kMaxSplits], ov[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++)
+    if (s < S) {
+      const float *ml = part_ml + ((((size_t)s * B + b) * H + h) * T + t) * 2;
+      mv[s] = ml[0];
+      lv[s] = ml[1];
+      ov[s] = part_o[((size_t)s * B + b) * T * d + (size_t)t * d + c];
+    }
   float M = -INFINITY;
-  for (int s = 0; s < S; s++) M = fmaxf(M, part_ml[((((size_t)s * B + b) * H + h) * T + t) * 2]);
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++)
+    if (s < S) M = fmaxf(M, mv[s]);
   float num = 0.0f, den = 0.0f;
-  for (int s = 0; s < S; s++) {
-    const float *ml = part_ml + ((((size_t)s * B + b) * H + h) * T + t) * 2;
-    const float f = ml[0] == -INFINITY ? 0.0f : expf(ml[0] - M);
-    num += part_o[((size_t)s * B + b) * T * d + (size_t)t * d + c] * f;
-    den += ml[1] * f;
-  }
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++)
+    if (s < S) {
+      const float f = mv[s] == -INFINITY ? 0.0f : expf(mv[s] - M);
+      num += ov[s] * f;
+      den += lv[s] * f;
+    }
   out[i] = num / den;
 }
 
@@ -753,7 +768,7 @@ hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, 
                          float *part_o, float *part_ml, uint16_t *kv_split, int n_cu, hipStream_t s) {
   if (d != H * kHd || T < 1 || !kv_split) return hipErrorInvalidValue;
   const int S = cfm_attn_splits(B, T, H, n_cu), tiles = (T + kAk - 1) / kAk, kts = (tiles + S - 1) / S;
-  if (S > 1 && (!part_o || !part_ml)) return hipErrorInvalidValue;
+  if (S > 8 || (S > 1 && (!part_o || !part_ml))) return hipErrorInvalidValue;  // the combine holds 8
   const int Tp = tiles * kAk;
   const long nthreads = (long)B * H * Tp * 8 + (long)B * H * (Tp / 8) * kHd;
   hipLaunchKernelGGL(kv_split_kernel, dim3(nblk(nthreads)), dim3(256), 0, s, qkv,
