@@ -554,8 +554,10 @@ struct Row8 {
     for (int i = 0; i < (KVT == kKvBf16 ? 4 : 8); i++) w[i] = 0u;
   }
   __device__ __forceinline__ float at(int e) const {
-    if constexpr (KVT == kKvBf16) return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
-    return __uint_as_float(w[e]);
+    if constexpr (KVT == kKvBf16)
+      return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+    else
+      return __uint_as_float(w[e]);
   }
 };
 
