@@ -67,6 +67,38 @@ def step_bytes(weight_bytes: int, L: int) -> int:
     return weight_bytes + KV_ROW_BYTES * L + KV_ROW_BYTES + 8194 * 4
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # fp16 dense, MI355X
+
+
+def prefill_flops(T: int, d=1280, F=5120, V=8194, layers=24, heads=20, hd=64) -> float:
+    """Algorithmic FLOPs of a T-row prefill (gpt.rs:636-696): the four linears of every
+    block over all rows, causal attention (QK^T and PV over the T(T+1)/2 visible pairs
+    of each head), and mel_head on the last row only."""
+    lin = 2.0 * T * layers * (d * 3 * d + d * d + d * F + F * d)
+    att = 2.0 * 2.0 * layers * heads * hd * (T * (T + 1) / 2)
+    return lin + att + 2.0 * d * V
+
+
+def ttft_roofline(ttft_ms: float, prefill_ms: float, T: int, weight_bytes: int) -> dict:
+    """Time to first token against its roofline: the prefill's algorithmic FLOPs at the
+    fp16 dense MFMA peak and its algorithmic bytes (every weight once, the T K/V rows
+    written, the logits) at the HBM peak; the bound is the larger of the two times."""
+    flop = prefill_flops(T)
+    nbytes = weight_bytes + KV_ROW_BYTES * T + 8194 * 4
+    t_mfma = flop / (MFMA_PEAK_TFLOPS * 1e12) * 1e3
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9) * 1e3
+    bound_ms = max(t_mfma, t_hbm)
+    return {"ttft_ms": round(ttft_ms, 3), "prefill_device_ms": round(prefill_ms, 3), "rows": T,
+            "flop": round(flop), "bytes": nbytes,
+            "bound": "mfma" if t_mfma >= t_hbm else "hbm",
+            "roofline_ms": round(bound_ms, 4),
+            "achieved_tflops": round(flop / (ttft_ms * 1e-3) / 1e12, 1),
+            "frac": round(bound_ms / ttft_ms, 4),
+            "frac_prefill_device": round(bound_ms / prefill_ms, 4),
+            "note": "frac = roofline time / time; ttft is host call to the first token id on the host "
+                    "(prefill + one sample), prefill_device_ms the prefill's HIP-event time"}
+
+
 def cpu_baseline(W, prompt, sp, n_steps: int, prior):
     """The oracle (CPU restatement of the reference decoder) on the same weights: the
     prompt's prefill (CPU time to first token), then, from a cache holding the prompt and
@@ -202,7 +234,7 @@ def f32_kv_decode(H, g, cp, sp, weight_bytes):
             "hbm_achieved_gbs": round(achieved, 1), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)}
 
 
-def batch_decode(H, synth, g, cfg, seed):
+def batch_decode(H, synth, g, cfg, seed, weight_bytes):
     """The batched workload: 8 sentences with text lengths U[20, 200] and decode lengths
     U[200, 1200] (seeded), each stopping at its own length (STOP masked until then),
     sampled (T 0.8, top-k 30, top-p 0.8, penalty 10), bf16 caches of 2048 rows.  One
@@ -225,14 +257,40 @@ def batch_decode(H, synth, g, cfg, seed):
     total = sum(len(c) for c in codes)
     assert [len(c) for c in codes] == [int(x) for x in n_dec]
     steps = int(n_dec.max())
-    print(f"[bench] batch-8 decode: {total / wall:.1f} tokens/s aggregate", file=sys.stderr, flush=True)
+    # the 8 prefills alone (the same prompts, host call time), so that the decode part of the
+    # call can be priced against HBM
+    t0 = time.perf_counter()
+    for b in range(8):
+        g.prefill(prompts[b].text_tokens, prompts[b].conds, prompts[b].lang_id, caches[b], logits=False)
+    prefill_s = time.perf_counter() - t0
+    decode_s = wall - prefill_s
+    # Algorithmic bytes of the batched steps: sequence b (prompt rows T_b = 32 + n_text + 3)
+    # makes n_dec - 1 steps, step i at T_b + i + 1 keys; every batched step streams the
+    # weights once, and each live sequence reads its K/V rows, writes one and its logits.
+    wb = weight_bytes
+    Tb = 32 + n_text + 3
+    n_steps = n_dec - 1
+    n_batched = int(n_steps.max())
+    kv_read = sum(KV_ROW_BYTES * (int(n_steps[b]) * int(Tb[b]) + int(n_steps[b]) * (int(n_steps[b]) + 1) // 2)
+                  for b in range(8))
+    per_seq_rest = (KV_ROW_BYTES + 8194 * 4) * int(n_steps.sum())
+    total_bytes = n_batched * wb + kv_read + per_seq_rest
+    gbs = total_bytes / decode_s / 1e9
+    print(f"[bench] batch-8 decode: {total / wall:.1f} tokens/s aggregate, {gbs:.0f} GB/s", file=sys.stderr,
+          flush=True)
     return {"workload": "batch 8 sentences, text lengths U[20,200], decode lengths U[200,1200] with per-sequence "
                         "stop, sampled (T 0.8, top-k 30, top-p 0.8, penalty 10), bf16 caches of 2048 rows",
             "text_lengths": [int(x) for x in n_text], "decode_lengths": [int(x) for x in n_dec],
             "tokens": total, "ms": round(wall * 1e3, 2),
             "aggregate_tokens_per_s": round(total / wall, 1),
             "per_sequence_tokens_per_s": round(steps / wall, 1),
-            "note": "host call time includes the 8 prefills; one batched step per token of the longest sequence"}
+            "prefills_ms": round(prefill_s * 1e3, 2), "decode_ms": round(decode_s * 1e3, 2),
+            "batched_steps": n_batched, "algorithmic_bytes": int(total_bytes),
+            "weight_bytes": int(n_batched * wb), "kv_read_bytes": int(kv_read),
+            "hbm_achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "host call time includes the 8 prefills; one batched step per token of the longest sequence; "
+                    "hbm figures: algorithmic bytes of the batched steps (weights once per step, each live "
+                    "sequence's K/V rows) / (call time - the 8 prefills' time)"}
 
 
 def int4_decode(H, synth, seed):
@@ -362,7 +420,7 @@ def main():
             print(f"[bench] cfm: {r['solve_ms']} ms per 25-step solve", flush=True)
             return
         if args.only == "batch8":
-            r = batch_decode(H, synth, g, cfg, args.seed)
+            r = batch_decode(H, synth, g, cfg, args.seed, weight_bytes)
             print(f"[bench] batch8: {r['aggregate_tokens_per_s']} tokens/s aggregate", flush=True)
             return
         if args.only == "decode":
@@ -465,6 +523,7 @@ def main():
                    "prefill_rows": T, "decode_tokens": n_tok, "step": "one full generation",
                    "decode_path": decode_path},
         "ttft_ms": round(ttft_ms, 3),
+        "ttft": ttft_roofline(ttft_ms, pre_ms, T, weight_bytes),
         "decode_tokens_per_s": round(dec_steps / (dec_ms * 1e-3), 2),
         "decode_step_us": round(step_ms * 1e3, 2),
         "prefill_ms": round(pre_ms, 3),
@@ -480,7 +539,7 @@ def main():
         out["secondary"] = {"short_decode": short_decode(H, synth, g, cfg, args.seed),
                             "f32_kv_decode": f32_kv_decode(H, g, cp, sp, weight_bytes),
                             "prefill_heavy": prefill_heavy(H, synth, g, cfg, args.seed),
-                            "batch8_decode": batch_decode(H, synth, g, cfg, args.seed)}
+                            "batch8_decode": batch_decode(H, synth, g, cfg, args.seed, weight_bytes)}
         del g, kv
         out["secondary"]["int4_decode"] = int4_decode(H, synth, args.seed)
         out["secondary"]["cfm_solve"] = cfm_solve(args.seed)

@@ -151,7 +151,8 @@ void *itts_gpt_stream(const itts_gpt *gpt);
 
 /* Decode-step implementation (no counterpart in the reference, whose step is one MLX
  * graph per token, gpt.rs:702-754).  AUTO: the persistent single-launch step wherever it
- * supports the shape (8-bit codes, bf16 cache, one block per compute unit), else the
+ * supports the shape (8- or 4-bit codes, fp16 or fp32 group params, bf16 or fp32 cache
+ * rows, at most 12 x 216 = 2,592 cache rows, one block per compute unit), else the
  * multi-kernel step.  MULTI forces the multi-kernel step; PERSISTENT makes caches that
  * cannot use it fail at creation.  Applies to caches created afterwards. */
 typedef enum itts_decode_path {
