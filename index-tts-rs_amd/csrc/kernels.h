@@ -175,6 +175,9 @@ struct PersistArgs {
   int n_layer, d, H, F, V, S, B;
   DevQL head;
   const float *ln_f_w, *ln_f_b, *fn_w, *fn_b;
+  // LayerNorms folded into the QKV and c_fc products (ln_fold_layout): per layer
+  // G = W.gamma and c = W.beta + bias of both products, fold_floats(d, F) floats a layer
+  const float *fold;
   const float *mel_emb, *mel_pos;
   void *kc, *vc;           // cache bases [n_layer][H][max_seq][64], bf16 or f32 rows
   int max_seq;
@@ -190,6 +193,16 @@ struct PersistArgs {
   // slice, row outputs, attention partials of one head, one layer's staged parameters
   int xin_len, part_len, own_len, out_len, pp_len, lp_len;
 };
+// A LayerNorm followed by a QuantizedLinear, y = W.((x - mu) * rstd * gamma + beta) + bias,
+// equals rstd * (W.(gamma * x) - mu * G) + c with G = W.gamma and c = W.beta + bias, so
+// the product can start on gamma * x before mu and rstd are known.  Per layer the fold
+// buffer holds G and c of c_attn (ln_1) and of c_fc (ln_2):
+//   [G_qkv 3d][c_qkv 3d][G_fc F][c_fc F]
+__host__ __device__ inline size_t fold_floats(int d, int F) { return 6 * (size_t)d + 2 * (size_t)F; }
+// G[o] = sum_k Wdeq[o][k] gamma[k] and c[o] = sum_k Wdeq[o][k] beta[k] + bias[o] for the N
+// rows of ql (fp64 sums, rounded once), one wave per row.
+hipError_t launch_ln_fold(const DevQL &ql, int bits, int ptype, const float *gamma, const float *beta, float *G,
+                          float *c, hipStream_t s);
 // Whether the persistent step supports this shape on B blocks; *S = attention splits.
 // f32 rows also need persist_f32_v_floats() floats from the start of the block's LDS
 // (input row, normalised row and partials: the host pads the partials to fit).

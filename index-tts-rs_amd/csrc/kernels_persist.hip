@@ -206,6 +206,30 @@ __device__ __forceinline__ bool poll_rows(const void *arr, int N, int B, const i
       });
 }
 
+// Pollers: poll_rows for the input of a folded LayerNorm: x into dst and gamma * x into
+// dst_g (gamma in LDS).
+__device__ __forceinline__ bool poll_rows_ln(const void *arr, int N, int B, const int *rs, uint32_t ep, float *dst,
+                                             float *dst_g, const float *gamma, uint32_t *err, int t) {
+  const int W = words_for((N + B - 1) / B);
+  const FastDiv divW(W);
+  const u32x4 *src = static_cast<const u32x4 *>(arr);
+  return poll(
+      B * W, ep, err, t, [&](int i) { return src + i; },
+      [&](int i, u32x4 v) {
+        const int s = divW(i), j = i - s * W;
+        const int r0 = rs[s], len = rs[s + 1] - r0;
+        const float f[3] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z)};
+#pragma unroll
+        for (int e = 0; e < 3; e++) {
+          const int k = 3 * j + e;
+          if (k < len) {
+            dst[r0 + k] = f[e];
+            dst_g[r0 + k] = gamma[r0 + k] * f[e];
+          }
+        }
+      });
+}
+
 // Publisher lane j < W: the block's rows (vals[0..rows)) as its segment of arr.
 __device__ inline void publish_rows(void *arr, int N, int B, int b, const float *vals, int rows, uint32_t ep,
                                     int lane) {
@@ -364,15 +388,15 @@ __device__ inline float wave64_max(float x) {
 // Loader waves sum the rows of part[] (a row is m.C chunk partials), in a fixed order:
 // rows of 256 chunks or more take a wave each (lane 0 calls epi), shorter rows 16 lanes
 // each, four rows per wave, rows lw*4.. of each pass of 9 waves (the last lane of a row
-// calls epi).  epi(row, value) receives the row value plus its bias (LDS).
+// calls epi).  epi(row, sum) receives the row's product without its bias.
 template <class Epi>
-__device__ inline void row_sums(const RowMap &m, const float *part, const float *bias, int lw, int lane, Epi epi) {
+__device__ inline void row_sums(const RowMap &m, const float *part, int lw, int lane, Epi epi) {
   if (m.C >= 256) {  // long rows: a wave per row
     for (int r = lw; r < m.rows; r += kLoadWaves) {
       float acc = 0.0f;
       for (int c = lane; c < m.C; c += 64) acc += part[r * m.C + c];
       acc = wave64_sum(acc);
-      if (lane == 0) epi(r, acc + bias[r]);
+      if (lane == 0) epi(r, acc);
     }
     return;
   }
@@ -383,15 +407,55 @@ __device__ inline void row_sums(const RowMap &m, const float *part, const float 
     if (r < m.rows)
       for (int c = sl; c < m.C; c += 16) acc += part[r * m.C + c];
     acc = row16_sum(acc);
-    if (sl == 15 && r < m.rows) epi(r, acc + bias[r]);
+    if (sl == 15 && r < m.rows) epi(r, acc);
   }
 }
 
+// ---- folded LayerNorm statistics ---------------------------------------------------------
+// Pollers: statistics of the LDS row x (n values, a multiple of 4, at most 4 * kPollThreads).
+// Poller wave w holds values 256w .. 256w + 255 (one float4 a lane) and writes their mean
+// and the sum of squared deviations from that mean (two passes over registers) to st[w]
+// and st[8 + w].
+__device__ __forceinline__ void ln_stats(const float *x, int n, float *st, int t) {
+  const int nq = n >> 2, w = t >> 6;
+  if (w * 64 >= nq) return;  // wave-uniform
+  const int cnt = min(64, nq - w * 64);
+  const bool act = t < nq;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (act) v = reinterpret_cast<const float4 *>(x)[t];
+  const float m = wave64_sum((v.x + v.y) + (v.z + v.w)) / (float)(4 * cnt);
+  float q = 0.0f;
+  if (act) {
+    const float d0 = v.x - m, d1 = v.y - m, d2 = v.z - m, d3 = v.w - m;
+    q = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+  }
+  q = wave64_sum(q);
+  if ((t & 63) == 0) {
+    st[w] = m;
+    st[8 + w] = q;
+  }
+}
+// (mean, rstd) of the row from the wave statistics, merged in wave order by the pairwise
+// update of Chan, Golub and LeVeque (1979); biased variance, eps 1e-5 (gpt.rs:339,375).
+__device__ inline float2 ln_stats_merge(const float *st, int n) {
+  const int nq = n >> 2, nw = (nq + 63) >> 6;
+  float na = (float)(4 * min(64, nq)), mean = st[0], m2 = st[8];
+  for (int w = 1; w < nw; w++) {
+    const float nb = (float)(4 * min(64, nq - 64 * w)), nt = na + nb, delta = st[w] - mean;
+    mean += delta * (nb / nt);
+    m2 += st[8 + w] + delta * delta * (na * nb / nt);
+    na = nt;
+  }
+  return make_float2(mean, 1.0f / sqrtf(m2 / (float)n + 1e-5f));
+}
+
 // ---- parameters -----------------------------------------------------------------------
-// Stages the LayerNorm parameters (4 x d) and the block's bias rows of layer l (or, for
-// l == n_layer, of the head) into one parameter buffer with LDS-DMA copies issued by one
+// Stages one layer's parameters into a parameter buffer with LDS-DMA copies issued by one
 // wave (lane in [0, 64)): no registers are written, and nothing waits for the copies until
 // the wave's own s_waitcnt, placed where the wave has slack.  d is a multiple of 64.
+// Layer l: [ln_1 gamma d][ln_2 gamma d] and the block's rows of c_qkv, G_qkv, the c_proj
+// bias, c_fc, G_fc and the mlp c_proj bias (folded LayerNorms: the betas live in c).
+// l == n_layer (the head): [ln_f w][ln_f b][final_norm w][final_norm b][mel_head bias rows].
 __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, float *lp, const RowMap &mq,
                                                  const RowMap &mp, const RowMap &mf, const RowMap &mm,
                                                  const RowMap &mh, int lane) {
@@ -399,26 +463,31 @@ __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, fl
   const int d = a.d;
   const bool head = l >= a.n_layer;
   const DevLayer *Ly = head ? nullptr : a.layers + l;
-  const float *v0 = head ? a.ln_f_w : Ly->ln1_w, *v1 = head ? a.ln_f_b : Ly->ln1_b;
-  const float *v2 = head ? a.fn_w : Ly->ln2_w, *v3 = head ? a.fn_b : Ly->ln2_b;
+  const int nv = head ? 4 : 2;
+#pragma unroll
   for (int arr = 0; arr < 4; arr++) {
-    const float *src = arr == 0 ? v0 : arr == 1 ? v1 : arr == 2 ? v2 : v3;
+    if (arr >= nv) break;
+    const float *src = head ? (arr == 0 ? a.ln_f_w : arr == 1 ? a.ln_f_b : arr == 2 ? a.fn_w : a.fn_b)
+                            : (arr == 0 ? Ly->ln1_w : Ly->ln2_w);
     for (int off = 0; off < d; off += 256)  // 64 lanes x 4 floats per copy
       if (off + lane * 4 < d) __builtin_amdgcn_global_load_lds(src + off + lane * 4, (lds_ptr)(lp + arr * d + off), 16, 0, 0);
   }
-  float *bl = lp + 4 * d;
-  auto rows = [&](const RowMap &m, const float *bias) {
+  float *bl = lp + nv * d;
+  auto rows = [&](const RowMap &m, const float *v) {
     for (int r0 = 0; r0 < m.rows; r0 += 64)
-      if (r0 + lane < m.rows) __builtin_amdgcn_global_load_lds(bias + m.row0 + r0 + lane, (lds_ptr)(bl + r0), 4, 0, 0);
+      if (r0 + lane < m.rows) __builtin_amdgcn_global_load_lds(v + m.row0 + r0 + lane, (lds_ptr)(bl + r0), 4, 0, 0);
     bl += m.rows;
   };
   if (head) {
     rows(mh, a.head.bias);
     return;
   }
-  rows(mq, Ly->attn.bias);
+  const float *fo = a.fold + fold_floats(d, a.F) * l;
+  rows(mq, fo + 3 * d);          // c_qkv
+  rows(mq, fo);                  // G_qkv
   rows(mp, Ly->proj.bias);
-  rows(mf, Ly->fc.bias);
+  rows(mf, fo + 6 * d + a.F);    // c_fc
+  rows(mf, fo + 6 * d);          // G_fc
   rows(mm, Ly->mproj.bias);
 }
 
@@ -527,8 +596,9 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   const RowMap m_fc = rows_of(F, d / EPC, b, B);
   const RowMap m_mp = rows_of(d, F / EPC, b, B);
   const RowMap m_head = rows_of(a.V, d / EPC, b, B);
-  // bias rows inside a layer's parameter buffer
-  const int bo_q = 4 * d, bo_p = bo_q + m_qkv.rows, bo_f = bo_p + m_proj.rows, bo_m = bo_f + m_fc.rows;
+  // rows inside a layer's parameter buffer (stage_params_dma)
+  const int bo_cq = 2 * d, bo_gq = bo_cq + m_qkv.rows, bo_p = bo_gq + m_qkv.rows, bo_cf = bo_p + m_proj.rows,
+            bo_gf = bo_cf + m_fc.rows, bo_m = bo_gf + m_fc.rows;
   const bool attn_block = b < H * S;
   const int ah = b / S, aj = b % S;
   const int j0 = (int)((long)L * aj / S), j1 = (int)((long)L * (aj + 1) / S);
@@ -569,16 +639,24 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     const DevLayer &Ly = a.layers[l];
     const uint32_t ep = ep0 + (uint32_t)l * 8u;
     const float *lp = lpb + (l & 1) * a.lp_len;
-    // ---------------- P1: LN1, QKV rows; K/V rows into the cache --------------------
+    // ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------
+    // The loaders start the product on gamma * x while the pollers form the row's
+    // statistics; the row sums apply them: rstd * (sum - mean * G) + c.
     if (l > 0) {
-      if (poller && !poll_rows(a.x_x, d, B, rs_d, ep - 8u + 6u, xin, err, T)) sh.abort = 1;
-      __syncthreads();
-      if (sh.abort) return;
+      if (poller && !poll_rows_ln(a.x_x, d, B, rs_d, ep - 8u + 6u, xin, xn, lp, err, T)) sh.abort = 1;
+    } else if (poller) {
+      for (int i = T; i < d; i += kPollThreads) xn[i] = lp[i] * xin[i];
     }
-    layer_norm(xin, xn, lp, lp + d, d, sh.red, T);
+    __syncthreads();
+    if (sh.abort) return;
+    if (poller) ln_stats(xin, d, sh.red, T);
     if (loader) dot_slots<BITS>(wq, m_qkv, xn, part, ll);
     __syncthreads();
-    if (loader) row_sums(m_qkv, part, lp + bo_q, lw, lane, [&](int r, float v) { out[r] = v; });
+    if (loader) {
+      const float2 st = ln_stats_merge(sh.red, d);
+      row_sums(m_qkv, part, lw, lane,
+               [&](int r, float v) { out[r] = st.y * (v - st.x * lp[bo_gq + r]) + lp[bo_cq + r]; });
+    }
     __syncthreads();
     if (pub) {
       publish_rows(a.x_qkv, 3 * d, B, b, out, m_qkv.rows, ep + 1u, lane);
@@ -876,8 +954,8 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (loader) dot_slots<BITS>(wp, m_proj, xin, part, ll);
     __syncthreads();
     if (loader)
-      row_sums(m_proj, part, lp + bo_p, lw, lane, [&](int r, float v) {
-        const float xm = own[r] + v;
+      row_sums(m_proj, part, lw, lane, [&](int r, float v) {
+        const float xm = own[r] + (v + lp[bo_p + r]);
         own_mid[r] = xm;
         out[r] = xm;
       });
@@ -887,13 +965,17 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // the row sums behind the memory pipeline)
     if (loader) load_slots<BITS, PT>(wm, Ly.mproj, m_mp, ll);
     // ---------------- P4: LN2, c_fc rows + GELU ------------------------------------
-    if (poller && !poll_rows(a.x_mid, d, B, rs_d, ep + 4u, xin, err, T)) sh.abort = 1;
+    if (poller && !poll_rows_ln(a.x_mid, d, B, rs_d, ep + 4u, xin, xn, lp + d, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    layer_norm(xin, xn, lp + 2 * d, lp + 3 * d, d, sh.red, T);
+    if (poller) ln_stats(xin, d, sh.red, T);
     if (loader) dot_slots<BITS>(wf, m_fc, xn, part, ll);
     __syncthreads();
-    if (loader) row_sums(m_fc, part, lp + bo_f, lw, lane, [&](int r, float v) { out[r] = gelu_tanh(v); });
+    if (loader) {
+      const float2 st = ln_stats_merge(sh.red, d);
+      row_sums(m_fc, part, lw, lane,
+               [&](int r, float v) { out[r] = gelu_tanh(st.y * (v - st.x * lp[bo_gf + r]) + lp[bo_cf + r]); });
+    }
     __syncthreads();
     if (pub) {
       publish_rows(a.x_f, F, B, b, out, m_fc.rows, ep + 5u, lane);
@@ -907,8 +989,8 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (loader) dot_slots<BITS>(wm, m_mp, xin, part, ll);
     __syncthreads();
     if (loader)
-      row_sums(m_mp, part, lp + bo_m, lw, lane, [&](int r, float v) {
-        const float xo = own_mid[r] + v;
+      row_sums(m_mp, part, lw, lane, [&](int r, float v) {
+        const float xo = own_mid[r] + (v + lp[bo_m + r]);
         own[r] = xo;
         out[r] = xo;
       });
@@ -929,7 +1011,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     layer_norm(xn, xn, lp + 2 * d, lp + 3 * d, d, sh.red, tid);
     if (loader) dot_slots<BITS>(wh, m_head, xn, part, ll);
     __syncthreads();
-    if (loader) row_sums(m_head, part, lp + 4 * d, lw, lane, [&](int r, float v) { out[r] = v; });
+    if (loader) row_sums(m_head, part, lw, lane, [&](int r, float v) { out[r] = v + lp[4 * d + r]; });
     __syncthreads();
     if (pub) {
       for (int r = lane; r < m_head.rows; r += 64) a.logits[m_head.row0 + r] = out[r];
@@ -976,8 +1058,73 @@ const void *persist_fn(int bits, int ptype, int kvt) {
 
 }  // namespace
 
+namespace {
+
+// One wave per row o of ql: G[o] = sum_k Wdeq[o][k] gamma[k], c[o] = sum_k Wdeq[o][k]
+// beta[k] + bias[o], with Wdeq = s * q + b of the row's 64-groups (gpt.rs:221-264), summed in
+// fp64 and rounded once.  Lane i takes columns i, i + 64, ... .
+template <int BITS, int PT>
+__global__ __launch_bounds__(256) void ln_fold_kernel(DevQL ql, const float *gamma, const float *beta, float *G,
+                                                      float *c) {
+  const int lane = threadIdx.x & 63;
+  const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (o >= ql.N) return;
+  const int K = ql.K, ng = K / kGroup;
+  double g_acc = 0.0, b_acc = 0.0;
+  for (int g = 0; g < ng; g++) {
+    float s, bb;
+    if constexpr (PT == kParamF16) {
+      const uint32_t w = static_cast<const uint32_t *>(ql.params)[(size_t)o * ng + g];
+      s = half_bits_to_float(w & 0xffffu);
+      bb = half_bits_to_float(w >> 16);
+    } else {
+      const float2 w = static_cast<const float2 *>(ql.params)[(size_t)o * ng + g];
+      s = w.x;
+      bb = w.y;
+    }
+    const int k = g * kGroup + lane;
+    uint32_t q;
+    if constexpr (BITS == 8)
+      q = ql.codes[(size_t)o * K + k];
+    else
+      q = (ql.codes[((size_t)o * K + k) >> 1] >> (4 * (k & 1))) & 0xfu;
+    const double w = (double)s * (double)q + (double)bb;
+    g_acc += w * (double)gamma[k];
+    b_acc += w * (double)beta[k];
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    g_acc += __shfl_xor(g_acc, m);
+    b_acc += __shfl_xor(b_acc, m);
+  }
+  if (lane == 0) {
+    G[o] = (float)g_acc;
+    c[o] = (float)(b_acc + (double)ql.bias[o]);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_ln_fold(const DevQL &ql, int bits, int ptype, const float *gamma, const float *beta, float *G,
+                          float *c, hipStream_t s) {
+  const dim3 grid((ql.N + 3) / 4), block(256);
+  if (bits == 4) {
+    if (ptype == kParamF16)
+      ln_fold_kernel<4, kParamF16><<<grid, block, 0, s>>>(ql, gamma, beta, G, c);
+    else
+      ln_fold_kernel<4, kParamF32><<<grid, block, 0, s>>>(ql, gamma, beta, G, c);
+  } else {
+    if (ptype == kParamF16)
+      ln_fold_kernel<8, kParamF16><<<grid, block, 0, s>>>(ql, gamma, beta, G, c);
+    else
+      ln_fold_kernel<8, kParamF32><<<grid, block, 0, s>>>(ql, gamma, beta, G, c);
+  }
+  return hipGetLastError();
+}
+
 bool persist_supported(int d, int F, int V, int H, int n_layer, int max_seq, int B, int bits, int *S_out) {
-  if (B < 1 || H < 1 || d % 64 != 0 || d > 4 * kThreads || F % 64 != 0 || n_layer < 1 || (bits != 8 && bits != 4))
+  // d <= 4 * kPollThreads: the folded LayerNorms' statistics take one float4 per poller lane
+  if (B < 1 || H < 1 || d % 64 != 0 || d > 4 * kPollThreads || F % 64 != 0 || n_layer < 1 ||
+      (bits != 8 && bits != 4))
     return false;
   const int epc = bits == 8 ? 16 : 32;
   const int S = std::min(12, B / H);

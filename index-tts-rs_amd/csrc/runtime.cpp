@@ -142,8 +142,9 @@ struct itts_gpt {
   std::vector<DevLayer> layers;
   DevBuf ln_f_w, ln_f_b, fn_w, fn_b;
   DevQL head{};
-  // persistent decode step: device copy of `layers`, blocks (one per compute unit)
-  DevBuf dlayers;
+  // persistent decode step: device copy of `layers`, the folded LayerNorm rows
+  // (fold_floats(d, F) per layer), blocks (one per compute unit)
+  DevBuf dlayers, fold;
   int n_cu = 0;
   int device = 0;
   bool persist_ok = false;  // kernels set up (int8 or int4 codes)
@@ -787,7 +788,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     a.own_len = r4(rp);
     a.out_len = r4(std::max({rq, rp, rf, rh}));
     a.pp_len = r4(S * 66);
-    a.lp_len = r4(4 * d + std::max(rq + rp + rf + rp, rh));
+    a.lp_len = r4(std::max(2 * d + 2 * rq + rp + 2 * rf + rp, 4 * d + rh));  // stage_params_dma
     a.kvt = kv->kvt;
     // f32 rows: V of a split is staged over the input row, normalised row and partials
     if (kv->kvt == kKvF32)
@@ -823,6 +824,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
   a.ln_f_b = g->ln_f_b.as<float>();
   a.fn_w = g->fn_w.as<float>();
   a.fn_b = g->fn_b.as<float>();
+  a.fold = g->fold.as<float>();
   a.mel_emb = g->mel_emb.as<float>();
   a.mel_pos = g->mel_pos.as<float>();
   a.kc = kv->k.p;
@@ -975,6 +977,21 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
     g->device = dev;
     g->persist_ok = (bits == 8 || bits == 4) && coop != 0 && persist_init() == hipSuccess;
+    if (g->persist_ok) {  // G and c of the products that follow ln_1 and ln_2
+      const size_t per = fold_floats(d, F);
+      if (g->fold.ensure(sizeof(float) * per * c.n_layer) != hipSuccess)
+        return fail(set_error(ITTS_E_DEVICE, "fold buffer allocation failed"));
+      for (int l = 0; l < c.n_layer; l++) {
+        const DevLayer &D = g->layers[l];
+        float *fo = g->fold.as<float>() + per * l;
+        if (launch_ln_fold(D.attn, bits, g->ptype(), D.ln1_w, D.ln1_b, fo, fo + 3 * d, g->stream) != hipSuccess ||
+            launch_ln_fold(D.fc, bits, g->ptype(), D.ln2_w, D.ln2_b, fo + 6 * d, fo + 6 * d + F, g->stream) !=
+                hipSuccess)
+          return fail(set_error(ITTS_E_DEVICE, "LayerNorm fold launch failed"));
+      }
+      if (hipStreamSynchronize(g->stream) != hipSuccess)
+        return fail(set_error(ITTS_E_DEVICE, "LayerNorm fold failed"));
+    }
     if (sampler_stage_init(dev) != hipSuccess)
       return fail(set_error(ITTS_E_DEVICE, "sampler staging area lookup failed"));
   }

@@ -3,10 +3,10 @@ csrc/kernels_persist.hip in which thread 0 of every block stamps the 100 MHz rea
 counter (s_memrealtime) at the phase barriers of one chosen layer, with
 itts_trace_read() to copy the stamps out and choose the next traced layer.
 
-Slots (per block): 0 layer start, 1 x in (poll done), 18 LN1 done, 2 QKV dot, 3 QKV row
-sums, 4 q/k/v in, 5 scores, 6 P.V, 9 attention in, 10 c_proj dot, 11 c_proj row sums,
-12 x_mid in, 19 LN2 done, 13 c_fc dot, 14 c_fc row sums (GELU), 15 x_f in, 16 mlp c_proj
-dot, 17 mlp row sums; 24 / 25 the shader clock (s_memtime) at slots 0 / 17; 26-28 and
+Slots (per block): 0 layer start, 1 x in (poll done), 2 QKV dot (and the folded LN1's
+statistics), 3 QKV row sums, 4 q/k/v in, 5 scores, 6 P.V, 9 attention in, 10 c_proj dot,
+11 c_proj row sums, 12 x_mid in, 13 c_fc dot (and LN2's statistics), 14 c_fc row sums
+(GELU), 15 x_f in, 16 mlp c_proj dot, 17 mlp row sums; 24 / 25 the shader clock (s_memtime) at slots 0 / 17; 26-28 and
 29-31 the first loader lane and the publisher around the QKV and c_fc dots.
 
 Usage: python3 instrument.py <kernels_persist.hip> <out.hip>; build.sh builds the library.
@@ -36,15 +36,12 @@ once('namespace itts {\n\nnamespace {\n',
 once('#include "kernels.h"',
      '#include "kernels.h"\n#define STAMP(i) do { if (T == 0 && l == g_trace_layer && b < 1024) '
      'g_trace[b][i] = __builtin_amdgcn_s_memrealtime(); } while (0)')
-once("// ---------------- P1: LN1, QKV rows; K/V rows into the cache --------------------",
-     "// ---------------- P1: LN1, QKV rows; K/V rows into the cache --------------------\n    STAMP(0);\n"
+once("// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------",
+     "// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------\n    STAMP(0);\n"
      "    if (T == 0 && l == g_trace_layer && b < 1024) g_trace[b][24] = __builtin_amdgcn_s_memtime();")
-stamp_after(r"poll_rows\(a\.x_x, d, B, rs_d, ep - 8u \+ 6u, xin, err, T\)\) sh\.abort = 1;\s*__syncthreads\(\);"
-            r"\s*if \(sh\.abort\) return;\s*\}", 1)
-stamp_after(r"layer_norm\(xin, xn, lp, lp \+ d, d, sh\.red, T\);", 18)
+stamp_after(r"xn\[i\] = lp\[i\] \* xin\[i\];\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 1)
 stamp_after(r"dot_slots<BITS>\(wq, m_qkv, xn, part, ll\);\s*__syncthreads\(\);", 2)
-stamp_after(r"row_sums\(m_qkv, part, lp \+ bo_q, lw, lane, \[&\]\(int r, float v\) \{ out\[r\] = v; \}\);"
-            r"\s*__syncthreads\(\);", 3)
+stamp_after(r"lp\[bo_cq \+ r\]; \}\);\s*\}\s*__syncthreads\(\);", 3)
 stamp_after(r"if \(!ok\) sh\.abort = 1;\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 4)
 stamp_after(r"if \(lane == 0\) sh\.m_w\[lw\] = mloc;\s*\}\s*__syncthreads\(\);", 5)
 stamp_after(r"if \(lane == 0\) sh\.l_w\[lw\] = lsum;\s*\}\s*__syncthreads\(\);", 6)
@@ -52,11 +49,10 @@ stamp_after(r"put_word\(xin \+ h \* 64, i - h \* kHeadWords, 64, v\);\s*\}\)\)\s
             r"\s*if \(sh\.abort\) return;", 9)
 stamp_after(r"dot_slots<BITS>\(wp, m_proj, xin, part, ll\);\s*__syncthreads\(\);", 10)
 stamp_after(r"out\[r\] = xm;\s*\}\);\s*__syncthreads\(\);", 11)
-stamp_after(r"poll_rows\(a\.x_mid, d, B, rs_d, ep \+ 4u, xin, err, T\)\) sh\.abort = 1;\s*__syncthreads\(\);"
+stamp_after(r"poll_rows_ln\(a\.x_mid, [^;]*\) sh\.abort = 1;\s*__syncthreads\(\);"
             r"\s*if \(sh\.abort\) return;", 12)
-stamp_after(r"layer_norm\(xin, xn, lp \+ 2 \* d, lp \+ 3 \* d, d, sh\.red, T\);", 19)
 stamp_after(r"dot_slots<BITS>\(wf, m_fc, xn, part, ll\);\s*__syncthreads\(\);", 13)
-stamp_after(r"out\[r\] = gelu_tanh\(v\); \}\);\s*__syncthreads\(\);", 14)
+stamp_after(r"lp\[bo_cf \+ r\]\); \}\);\s*\}\s*__syncthreads\(\);", 14)
 stamp_after(r"poll_rows\(a\.x_f, [^;]*\) sh\.abort = 1;[^\n]*\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 15)
 stamp_after(r"dot_slots<BITS>\(wm, m_mp, xin, part, ll\);\s*__syncthreads\(\);", 16)
 stamp_after(r"own\[r\] = xo;\s*out\[r\] = xo;\s*\}\);\s*__syncthreads\(\);", 17)

@@ -19,10 +19,10 @@ import numpy as np  # noqa: E402
 import itts_hip as H  # noqa: E402
 from itts_hip import synth  # noqa: E402
 
-PHASES = [(0, "layer start"), (1, "x all-gather in"), (18, "LN1"), (2, "QKV dot"), (3, "QKV row sums"),
+PHASES = [(0, "layer start"), (1, "x all-gather in"), (2, "QKV dot + LN1 statistics"), (3, "QKV row sums"),
           (4, "q/k/v in (attention blocks)"), (5, "scores"), (6, "P.V"), (9, "attention all-gather in"),
-          (10, "c_proj dot"), (11, "c_proj row sums + residual"), (12, "x_mid all-gather in"), (19, "LN2"),
-          (13, "c_fc dot"), (14, "c_fc row sums + GELU"), (15, "x_f all-gather in"), (16, "mlp c_proj dot"),
+          (10, "c_proj dot"), (11, "c_proj row sums + residual"), (12, "x_mid all-gather in"),
+          (13, "c_fc dot + LN2 statistics"), (14, "c_fc row sums + GELU"), (15, "x_f all-gather in"), (16, "mlp c_proj dot"),
           (17, "mlp row sums + residual")]
 
 

@@ -13,8 +13,8 @@ def test_instrument_applies(tmp_path):
                         os.path.join(ROOT, "index-tts-rs_amd", "csrc", "kernels_persist.hip"), str(out)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
-    assert "18 phase stamps" in r.stdout
+    assert "16 phase stamps" in r.stdout
     text = out.read_text()
     assert 'extern "C" int itts_trace_read' in text
-    for i in (0, 1, 2, 3, 4, 5, 6, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19):
+    for i in (0, 1, 2, 3, 4, 5, 6, 9, 10, 11, 12, 13, 14, 15, 16, 17):
         assert f"STAMP({i});" in text
