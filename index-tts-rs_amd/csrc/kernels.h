@@ -189,9 +189,11 @@ struct PersistArgs {
   uint32_t *err;           // nonzero after a timed-out wait
   float *logits;           // [V]
   uint32_t ep_stride;      // epochs per step: 8 * (n_layer + 1)
-  // LDS region sizes (floats, multiples of 4): input row, per-chunk partials, residual
-  // slice, row outputs, attention partials of one head, one layer's staged parameters
-  int xin_len, part_len, own_len, out_len, pp_len, lp_len;
+  // LDS region sizes (floats, multiples of 4): input row, normalised row (both long enough
+  // for the dot products' padded layout: 4 floats after every 16-byte code chunk's
+  // values), per-chunk partials, residual slice, row outputs, attention partials of one
+  // head, one layer's staged parameters
+  int xin_len, xn_len, part_len, own_len, out_len, pp_len, lp_len;
 };
 // A LayerNorm followed by a QuantizedLinear, y = W.((x - mu) * rstd * gamma + beta) + bias,
 // equals rstd * (W.(gamma * x) - mu * G) + c with G = W.gamma and c = W.beta + bias, so

@@ -78,6 +78,16 @@ __device__ inline RowMap rows_of(int N, int C, int b, int B) {
 // The block whose rows contain row r: the largest b with row_start(N, b, B) <= r.
 __device__ inline int block_of(int N, int r, int B) { return (int)(((long)(r + 1) * B - 1) / N); }
 __device__ inline int words_for(int n) { return (n + 2) / 3; }
+
+// Activation rows as the dot products read them: every 16-byte code chunk's EPC values (16
+// int8 or 32 int4 codes) followed by 4 floats of padding.  Loader lanes take consecutive
+// chunks, so without the padding a wave's float4 reads would sit 64 (128) bytes apart and
+// fall into a quarter (an eighth) of the LDS banks; 80 (144) bytes apart, 16 consecutive
+// lanes cover every bank once.  Value k of a row sits at xpad(k).
+template <int BITS>
+__device__ inline int xpad(int k) {
+  return k + ((k >> (BITS == 8 ? 4 : 5)) << 2);
+}
 // i / d for 0 <= i < 2^16 and 1 <= d <= 2^15: one multiply-high by m = floor((2^32-1)/d) + 1.
 // i*m/2^32 exceeds i/d by i*(m - 2^32/d)/2^32 < i/2^32, below the 1/d gap to the next
 // integer for these ranges, so the floor is exact.
@@ -191,7 +201,9 @@ __device__ inline void put_word(float *dst, int j, int len, u32x4 v) {
 }
 
 // Pollers: the whole N-vector published by blocks (block s's rows as one segment of W
-// words) into dst[0..N); rs[s] = row_start(N, s, B) for s in [0, B] (LDS table).
+// words) into dst, in row order or (PAD) in the dot products' padded layout; rs[s] =
+// row_start(N, s, B) for s in [0, B] (LDS table).
+template <int BITS, bool PAD>
 __device__ __forceinline__ bool poll_rows(const void *arr, int N, int B, const int *rs, uint32_t ep, float *dst,
                                           uint32_t *err, int t) {
   const int W = words_for((N + B - 1) / B);
@@ -201,13 +213,19 @@ __device__ __forceinline__ bool poll_rows(const void *arr, int N, int B, const i
       B * W, ep, err, t, [&](int i) { return src + i; },
       [&](int i, u32x4 v) {
         const int s = divW(i), j = i - s * W;
-        const int r0 = rs[s];
-        put_word(dst + r0, j, rs[s + 1] - r0, v);
+        const int r0 = rs[s], len = rs[s + 1] - r0;
+        const float f[3] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z)};
+#pragma unroll
+        for (int e = 0; e < 3; e++) {
+          const int k = r0 + 3 * j + e;
+          if (3 * j + e < len) dst[PAD ? xpad<BITS>(k) : k] = f[e];
+        }
       });
 }
 
-// Pollers: poll_rows for the input of a folded LayerNorm: x into dst and gamma * x into
-// dst_g (gamma in LDS).
+// Pollers: poll_rows for the input of a folded LayerNorm: x into dst in row order and
+// gamma * x (gamma in LDS) into dst_g in the dot products' padded layout.
+template <int BITS>
 __device__ __forceinline__ bool poll_rows_ln(const void *arr, int N, int B, const int *rs, uint32_t ep, float *dst,
                                              float *dst_g, const float *gamma, uint32_t *err, int t) {
   const int W = words_for((N + B - 1) / B);
@@ -224,7 +242,7 @@ __device__ __forceinline__ bool poll_rows_ln(const void *arr, int N, int B, cons
           const int k = 3 * j + e;
           if (k < len) {
             dst[r0 + k] = f[e];
-            dst_g[r0 + k] = gamma[r0 + k] * f[e];
+            dst_g[xpad<BITS>(r0 + k)] = gamma[r0 + k] * f[e];
           }
         }
       });
@@ -328,7 +346,7 @@ __device__ inline float2 dot16(const u32x4 c, const float *xc) {
 }
 
 // Loaders: per-chunk partial products into part[] (LDS): scale * sum(code*x) + bias *
-// sum(x), the group affine folded per 16-value chunk.
+// sum(x), the group affine folded per 16-value chunk; xn in the padded layout (xpad).
 template <int BITS, int PT, int NS>
 __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const float *xn, float *part, int ll) {
   const int total = m.rows * m.C;
@@ -342,7 +360,7 @@ __device__ inline void dot_slots(const Slots<PT, NS> &s, const RowMap &m, const 
     if (c < total) {
       const int kc = c % m.C;
       const float2 p = param_value(s.p[j]);
-      const float2 r = BITS == 8 ? dot16(s.c[j], xn + kc * 16) : dot32(s.c[j], xn + kc * 32);
+      const float2 r = BITS == 8 ? dot16(s.c[j], xn + kc * 20) : dot32(s.c[j], xn + kc * 36);
       part[c] = p.x * r.x + p.y * r.y;
     }
     // one chunk's activations in registers at a time
@@ -412,41 +430,49 @@ __device__ inline void row_sums(const RowMap &m, const float *part, int lw, int 
 }
 
 // ---- folded LayerNorm statistics ---------------------------------------------------------
-// Pollers: statistics of the LDS row x (n values, a multiple of 4, at most 4 * kPollThreads).
-// Poller wave w holds values 256w .. 256w + 255 (one float4 a lane) and writes their mean
-// and the sum of squared deviations from that mean (two passes over registers) to st[w]
-// and st[8 + w].
-__device__ __forceinline__ void ln_stats(const float *x, int n, float *st, int t) {
-  const int nq = n >> 2, w = t >> 6;
-  if (w * 64 >= nq) return;  // wave-uniform
-  const int cnt = min(64, nq - w * 64);
+// Pollers, beside the other waves' products: mean and rstd of the LDS row x (n values, a
+// multiple of 4, at most 4 * kPollThreads; biased variance, eps 1e-5, gpt.rs:339,375) into
+// st[24], st[25].  Poller wave w holds values 256w .. 256w + 255 (one float4 a lane) and
+// writes their sum, mean and sum of squared deviations from that mean (two passes over
+// registers) to st[w], st[8 + w], st[16 + w]; the last wave to finish (a wrapping LDS
+// counter, zero between uses) merges them in wave order: mean = sum / n, and the squared
+// deviations from it are each wave's own plus count * (wave mean - mean)^2 (the parallel
+// form of the two-pass variance, Chan, Golub and LeVeque 1979).
+__device__ __forceinline__ void ln_stats(const float *x, int n, float *st, uint32_t *cnt, int t) {
+  const int nq = n >> 2, nw = (nq + 63) >> 6, w = t >> 6, lane = t & 63;
+  if (w >= nw) return;  // wave-uniform
   const bool act = t < nq;
   float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (act) v = reinterpret_cast<const float4 *>(x)[t];
-  const float m = wave64_sum((v.x + v.y) + (v.z + v.w)) / (float)(4 * cnt);
+  const float sum = wave64_sum((v.x + v.y) + (v.z + v.w));
+  const float m = sum / (float)(4 * min(64, nq - w * 64));
   float q = 0.0f;
   if (act) {
     const float d0 = v.x - m, d1 = v.y - m, d2 = v.z - m, d3 = v.w - m;
     q = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
   }
   q = wave64_sum(q);
-  if ((t & 63) == 0) {
-    st[w] = m;
-    st[8 + w] = q;
+  uint32_t old = 0;
+  if (lane == 0) {
+    st[w] = sum;
+    st[8 + w] = m;
+    st[16 + w] = q;
+    // a wave's LDS operations complete in order: the partials land before the count
+    old = atomicInc(cnt, (uint32_t)(nw - 1));
   }
-}
-// (mean, rstd) of the row from the wave statistics, merged in wave order by the pairwise
-// update of Chan, Golub and LeVeque (1979); biased variance, eps 1e-5 (gpt.rs:339,375).
-__device__ inline float2 ln_stats_merge(const float *st, int n) {
-  const int nq = n >> 2, nw = (nq + 63) >> 6;
-  float na = (float)(4 * min(64, nq)), mean = st[0], m2 = st[8];
-  for (int w = 1; w < nw; w++) {
-    const float nb = (float)(4 * min(64, nq - 64 * w)), nt = na + nb, delta = st[w] - mean;
-    mean += delta * (nb / nt);
-    m2 += st[8 + w] + delta * delta * (na * nb / nt);
-    na = nt;
+  if (__builtin_amdgcn_readfirstlane(old) != (uint32_t)(nw - 1)) return;
+  float s = 0.0f;
+  for (int i = 0; i < nw; i++) s += st[i];
+  const float mean = s / (float)n;
+  float m2 = 0.0f;
+  for (int i = 0; i < nw; i++) {
+    const float dm = st[8 + i] - mean;
+    m2 += st[16 + i] + (float)(4 * min(64, nq - 64 * i)) * (dm * dm);
   }
-  return make_float2(mean, 1.0f / sqrtf(m2 / (float)n + 1e-5f));
+  if (lane == 0) {
+    st[24] = mean;
+    st[25] = 1.0f / sqrtf(m2 / (float)n + 1e-5f);
+  }
 }
 
 // ---- parameters -----------------------------------------------------------------------
@@ -497,8 +523,11 @@ __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, fl
 // all three issued together, so the row is read once and every later pass works from
 // registers.  The waves holding values form the sums; every wave adds the wave sums in the
 // same order.
+// With q4 > 0, y is written in the dot products' padded layout (a float4 of padding after
+// every 2^q4 float4s) instead of row order; y may still be x, since every thread reads its
+// values before the first barrier and writes after the second.
 __device__ __forceinline__ void layer_norm(const float *x, float *y, const float *w, const float *b, int n, float *red,
-                                           int tid) {
+                                           int tid, int q4 = 0) {
   const int nq = n >> 2, nwv = (nq + 63) >> 6;
   const bool act = tid < nq, wact = tid < nwv * 64;
   float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), wv = xv, bv = xv;
@@ -535,15 +564,16 @@ __device__ __forceinline__ void layer_norm(const float *x, float *y, const float
     yv.y = (xv.y - mean) * rstd * wv.y + bv.y;
     yv.z = (xv.z - mean) * rstd * wv.z + bv.z;
     yv.w = (xv.w - mean) * rstd * wv.w + bv.w;
-    reinterpret_cast<float4 *>(y)[tid] = yv;
+    reinterpret_cast<float4 *>(y)[q4 > 0 ? tid + (tid >> q4) : tid] = yv;
   }
   __syncthreads();
 }
 
-struct PersistShared {
+struct __attribute__((aligned(16))) PersistShared {
   float red[32];
   int abort;
   int last;
+  uint32_t stat_cnt;  // folded LayerNorm statistics: waves done (wraps to 0)
   float m_w[kLoadWaves], l_w[kLoadWaves];
 };
 
@@ -570,12 +600,12 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
   u32x4 *x_part = static_cast<u32x4 *>(a.x_part);
   u32x4 *x_attn = static_cast<u32x4 *>(a.x_attn);
 
-  // LDS (floats): xin[xin_len] | xn[d] | part[part_len] | own[own_len] | own_mid[own_len] |
+  // LDS (floats): xin[xin_len] | xn[xn_len] | part[part_len] | own[own_len] | own_mid[own_len] |
   // out[out_len] | qs[64] | kn[64] | vn[64] | pp[S*66] | lp[2][lp_len] | kvs[2*3*576*4] |
   // rs[3][B+1] (int); the host rounds every length to a multiple of 4
   float *xin = lds;
   float *xn = xin + a.xin_len;
-  float *part = xn + d;
+  float *part = xn + a.xn_len;
   float *own = part + a.part_len;
   float *own_mid = own + a.own_len;
   float *out = own_mid + a.own_len;
@@ -643,19 +673,19 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // The loaders start the product on gamma * x while the pollers form the row's
     // statistics; the row sums apply them: rstd * (sum - mean * G) + c.
     if (l > 0) {
-      if (poller && !poll_rows_ln(a.x_x, d, B, rs_d, ep - 8u + 6u, xin, xn, lp, err, T)) sh.abort = 1;
+      if (poller && !poll_rows_ln<BITS>(a.x_x, d, B, rs_d, ep - 8u + 6u, xin, xn, lp, err, T)) sh.abort = 1;
     } else if (poller) {
-      for (int i = T; i < d; i += kPollThreads) xn[i] = lp[i] * xin[i];
+      for (int i = T; i < d; i += kPollThreads) xn[xpad<BITS>(i)] = lp[i] * xin[i];
     }
     __syncthreads();
     if (sh.abort) return;
-    if (poller) ln_stats(xin, d, sh.red, T);
+    if (poller) ln_stats(xin, d, sh.red, &sh.stat_cnt, T);
     if (loader) dot_slots<BITS>(wq, m_qkv, xn, part, ll);
     __syncthreads();
     if (loader) {
-      const float2 st = ln_stats_merge(sh.red, d);
+      const float mu = sh.red[24], rstd = sh.red[25];
       row_sums(m_qkv, part, lw, lane,
-               [&](int r, float v) { out[r] = st.y * (v - st.x * lp[bo_gq + r]) + lp[bo_cq + r]; });
+               [&](int r, float v) { out[r] = rstd * (v - mu * lp[bo_gq + r]) + lp[bo_cq + r]; });
     }
     __syncthreads();
     if (pub) {
@@ -946,7 +976,11 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
                       H * kHeadWords, ep + 3u, err, T, [&](int i) { return x_attn + i; },
                       [&](int i, u32x4 v) {
                         const int h = i / kHeadWords;
-                        put_word(xin + h * 64, i - h * kHeadWords, 64, v);
+                        const int j = i - h * kHeadWords;
+                        const float f[3] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z)};
+#pragma unroll
+                        for (int e = 0; e < 3; e++)
+                          if (3 * j + e < 64) xin[xpad<BITS>(h * 64 + 3 * j + e)] = f[e];
                       }))
       sh.abort = 1;
     __syncthreads();
@@ -965,16 +999,16 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // the row sums behind the memory pipeline)
     if (loader) load_slots<BITS, PT>(wm, Ly.mproj, m_mp, ll);
     // ---------------- P4: LN2, c_fc rows + GELU ------------------------------------
-    if (poller && !poll_rows_ln(a.x_mid, d, B, rs_d, ep + 4u, xin, xn, lp + d, err, T)) sh.abort = 1;
+    if (poller && !poll_rows_ln<BITS>(a.x_mid, d, B, rs_d, ep + 4u, xin, xn, lp + d, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
-    if (poller) ln_stats(xin, d, sh.red, T);
+    if (poller) ln_stats(xin, d, sh.red, &sh.stat_cnt, T);
     if (loader) dot_slots<BITS>(wf, m_fc, xn, part, ll);
     __syncthreads();
     if (loader) {
-      const float2 st = ln_stats_merge(sh.red, d);
+      const float mu = sh.red[24], rstd = sh.red[25];
       row_sums(m_fc, part, lw, lane,
-               [&](int r, float v) { out[r] = gelu_tanh(st.y * (v - st.x * lp[bo_gf + r]) + lp[bo_cf + r]); });
+               [&](int r, float v) { out[r] = gelu_tanh(rstd * (v - mu * lp[bo_gf + r]) + lp[bo_cf + r]); });
     }
     __syncthreads();
     if (pub) {
@@ -983,7 +1017,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     }
     if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
     // ---------------- P5: mlp c_proj rows + residual ---------------------------------
-    if (poller && !poll_rows(a.x_f, F, B, rs_f, ep + 5u, xin, err, T)) sh.abort = 1;
+    if (poller && !poll_rows<BITS, true>(a.x_f, F, B, rs_f, ep + 5u, xin, err, T)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
     if (loader) dot_slots<BITS>(wm, m_mp, xin, part, ll);
@@ -1004,11 +1038,11 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (loader) load_slots<BITS, PT>(wh, a.head, m_head, ll);
     const uint32_t ep = ep0 + (uint32_t)(a.n_layer - 1) * 8u;
     const float *lp = lpb + (a.n_layer & 1) * a.lp_len;
-    if (poller && !poll_rows(a.x_x, d, B, rs_d, ep + 6u, xin, err, tid)) sh.abort = 1;
+    if (poller && !poll_rows<BITS, false>(a.x_x, d, B, rs_d, ep + 6u, xin, err, tid)) sh.abort = 1;
     __syncthreads();
     if (sh.abort) return;
     layer_norm(xin, xn, lp, lp + d, d, sh.red, tid);
-    layer_norm(xn, xn, lp + 2 * d, lp + 3 * d, d, sh.red, tid);
+    layer_norm(xn, xn, lp + 2 * d, lp + 3 * d, d, sh.red, tid, BITS == 8 ? 2 : 3);
     if (loader) dot_slots<BITS>(wh, m_head, xn, part, ll);
     __syncthreads();
     if (loader) row_sums(m_head, part, lw, lane, [&](int r, float v) { out[r] = v + lp[4 * d + r]; });
@@ -1029,11 +1063,13 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
 template <int BITS, int PT, int KVF>
 __global__ __launch_bounds__(kThreads) void decode_persist_kernel(PersistArgs a) {
   __shared__ PersistShared sh;
-  extern __shared__ float lds[];
+  // 16-byte aligned: the float4 LDS accesses assume it (the dynamic region follows sh)
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   if (a.ctl->done) return;
   if (threadIdx.x == 0) {
     sh.abort = 0;
     sh.last = 0;
+    sh.stat_cnt = 0;
   }
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (wave >= kLoadWave0)
@@ -1154,7 +1190,7 @@ size_t persist_exchange_words(int d, int F, int H, int S, int B, size_t off[6]) 
 }
 
 size_t persist_lds_bytes(const PersistArgs &a) {
-  const size_t f = (size_t)a.xin_len + a.d + a.part_len + 2 * (size_t)a.own_len + a.out_len + 3 * 64 + a.pp_len +
+  const size_t f = (size_t)a.xin_len + a.xn_len + a.part_len + 2 * (size_t)a.own_len + a.out_len + 3 * 64 + a.pp_len +
                    2 * (size_t)a.lp_len + 2 * kKeyPasses * kLoadThreads * 4 + 3 * (size_t)(a.B + 1);
   return f * sizeof(float);
 }

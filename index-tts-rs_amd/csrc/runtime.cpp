@@ -782,8 +782,10 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     auto r4 = [](int n) { return (n + 3) & ~3; };
     auto rows = [&](int N) { return (N + B - 1) / B; };
     const int rq = rows(3 * d), rp = rows(d), rf = rows(F), rh = rows(V);
-    a.xin_len = std::max(d, F);
     const int epc = c.quant_bits == 8 ? 16 : 32;  // codes per 16-byte chunk
+    auto padded = [&](int n) { return r4(n + n / epc * 4); };  // 4 floats after each chunk's values
+    a.xin_len = padded(std::max(d, F));
+    a.xn_len = padded(d);
     a.part_len = r4(std::max({rq * (d / epc), rp * (d / epc), rf * (d / epc), rp * (F / epc), rh * (d / epc)}));
     a.own_len = r4(rp);
     a.out_len = r4(std::max({rq, rp, rf, rh}));
@@ -792,7 +794,7 @@ itts_status setup_persist(itts_gpt *g, itts_kv *kv, bool *used) {
     a.kvt = kv->kvt;
     // f32 rows: V of a split is staged over the input row, normalised row and partials
     if (kv->kvt == kKvF32)
-      a.part_len = std::max(a.part_len, r4(persist_f32_v_floats(kv->max_seq, S) - a.xin_len - d));
+      a.part_len = std::max(a.part_len, r4(persist_f32_v_floats(kv->max_seq, S) - a.xin_len - a.xn_len));
   }
   bool ok = shape_ok && persist_lds_bytes(a) <= kPersistMaxLds;
   if (ok) HIP_TRY(persist_fits(c.quant_bits, g->ptype(), kv->kvt, persist_lds_bytes(a), &ok));  // one block per CU

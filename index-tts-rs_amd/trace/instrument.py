@@ -39,21 +39,21 @@ once('#include "kernels.h"',
 once("// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------",
      "// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------\n    STAMP(0);\n"
      "    if (T == 0 && l == g_trace_layer && b < 1024) g_trace[b][24] = __builtin_amdgcn_s_memtime();")
-stamp_after(r"xn\[i\] = lp\[i\] \* xin\[i\];\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 1)
+stamp_after(r"\] = lp\[i\] \* xin\[i\];\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 1)
 stamp_after(r"dot_slots<BITS>\(wq, m_qkv, xn, part, ll\);\s*__syncthreads\(\);", 2)
 stamp_after(r"lp\[bo_cq \+ r\]; \}\);\s*\}\s*__syncthreads\(\);", 3)
 stamp_after(r"if \(!ok\) sh\.abort = 1;\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 4)
 stamp_after(r"if \(lane == 0\) sh\.m_w\[lw\] = mloc;\s*\}\s*__syncthreads\(\);", 5)
 stamp_after(r"if \(lane == 0\) sh\.l_w\[lw\] = lsum;\s*\}\s*__syncthreads\(\);", 6)
-stamp_after(r"put_word\(xin \+ h \* 64, i - h \* kHeadWords, 64, v\);\s*\}\)\)\s*sh\.abort = 1;\s*__syncthreads\(\);"
+stamp_after(r"xin\[xpad<BITS>\(h \* 64 \+ 3 \* j \+ e\)\] = f\[e\];\s*\}\)\)\s*sh\.abort = 1;\s*__syncthreads\(\);"
             r"\s*if \(sh\.abort\) return;", 9)
 stamp_after(r"dot_slots<BITS>\(wp, m_proj, xin, part, ll\);\s*__syncthreads\(\);", 10)
 stamp_after(r"out\[r\] = xm;\s*\}\);\s*__syncthreads\(\);", 11)
-stamp_after(r"poll_rows_ln\(a\.x_mid, [^;]*\) sh\.abort = 1;\s*__syncthreads\(\);"
+stamp_after(r"poll_rows_ln<BITS>\(a\.x_mid, [^;]*\) sh\.abort = 1;\s*__syncthreads\(\);"
             r"\s*if \(sh\.abort\) return;", 12)
 stamp_after(r"dot_slots<BITS>\(wf, m_fc, xn, part, ll\);\s*__syncthreads\(\);", 13)
 stamp_after(r"lp\[bo_cf \+ r\]\); \}\);\s*\}\s*__syncthreads\(\);", 14)
-stamp_after(r"poll_rows\(a\.x_f, [^;]*\) sh\.abort = 1;[^\n]*\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 15)
+stamp_after(r"poll_rows<BITS, true>\(a\.x_f, [^;]*\) sh\.abort = 1;[^\n]*\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 15)
 stamp_after(r"dot_slots<BITS>\(wm, m_mp, xin, part, ll\);\s*__syncthreads\(\);", 16)
 stamp_after(r"own\[r\] = xo;\s*out\[r\] = xo;\s*\}\);\s*__syncthreads\(\);", 17)
 once("    STAMP(17);", "    STAMP(17);\n    if (T == 0 && l == g_trace_layer && b < 1024) g_trace[b][25] = __builtin_amdgcn_s_memtime();")
