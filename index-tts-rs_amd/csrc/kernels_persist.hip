@@ -8,10 +8,11 @@
 // overlaps the dependency chain; what is left per phase is the exchange of the phase's
 // output vector between blocks.
 //
-// Exchange.  Values travel in 16-byte words: three fp32 values and an epoch, written by
-// one lane with one store and read with one load, both device-coherent.  A reader polls
-// the words it needs until each carries the phase's epoch, so no fence or grid barrier is
-// needed and a stale word is never taken for a fresh one.  A producer's values form one
+// Exchange.  Values travel in 16-byte words: three fp32 values and the epoch's low bits in
+// each 8-byte half (xstore), written by one lane with one store and read with one load,
+// both device-coherent.  A reader polls the words it needs until both halves of each carry
+// the phase's epoch, so no fence or grid barrier is needed and a stale (or partly stale)
+// word is never taken for a fresh one.  A producer's values form one
 // segment of ceil(len/3) words.  Epoch of (step s, layer l, phase p):
 // s * 8 * (n_layer + 1) + 8 * l + p + 1, with s from the control block.  A word is
 // rewritten only after every block has consumed it: the next write of any array depends
@@ -111,9 +112,23 @@ __device__ inline T gld(const void *p) {
 }
 
 // ---- exchange words --------------------------------------------------------------------
-// One device-coherent 16-byte store: values a, b, c and the epoch in the last dword.
+// A word holds three values and the epoch's low 16 bits twice, once in each 8-byte half:
+//   dword 0: a | dword 1: c bits 0-15, epoch bits 16-31 | dword 2: b | dword 3: c bits
+//   16-31, epoch bits 16-31.
+// No AMD document promises that a 16-byte store is observed whole by a 16-byte load (the
+// memory model's single-copy atomicity stops at 64 bits, for aligned 8-byte accesses), so
+// each half carries the epoch and a reader takes a word only when both halves do: a load
+// that saw one half of an older word fails and is polled again.  A word is rewritten at
+// most 200 epochs (one step) after it was last written, so 16 bits tell the expected epoch
+// from any earlier one; epochs restart at 1 when the exchange memory is cleared.
+__device__ inline uint32_t xtag(uint32_t ep) { return ep << 16; }
+__device__ inline bool xword_ok(const u32x4 w, uint32_t tag) { return ((w.y ^ tag) | (w.w ^ tag)) < 0x10000u; }
+// (a, b, c, 0) of a word that checked.
+__device__ inline u32x4 xword_vals(const u32x4 w) { return u32x4{w.x, w.z, (w.y & 0xffffu) | (w.w << 16), 0u}; }
+// One device-coherent 16-byte store of values a, b, c at epoch ep.
 __device__ inline void xstore(u32x4 *p, float a, float b, float c, uint32_t ep) {
-  const u32x4 v = {__float_as_uint(a), __float_as_uint(b), __float_as_uint(c), ep};
+  const uint32_t uc = __float_as_uint(c), tag = xtag(ep);
+  const u32x4 v = {__float_as_uint(a), (uc & 0xffffu) | tag, __float_as_uint(b), (uc >> 16) | tag};
   asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
 
@@ -162,12 +177,14 @@ __device__ __forceinline__ bool poll_k(int nw, uint32_t ep, uint32_t *err, int t
       p[k] = addr(i < nw ? i : base);
     }
     u32x4 w[K];
+    const uint32_t tag = xtag(ep);
     long spins = 0;
     while (true) {
       xload<K>(w, p);
       bool all = true;
 #pragma unroll
-      for (int k = 0; k < K; k++) all = all && (base + t + k * kPollThreads >= nw || w[k].w == ep);
+      for (int k = 0; k < K; k++)  // bitwise, not short-circuit: no branch per word
+        all = all & ((base + t + k * kPollThreads >= nw) | xword_ok(w[k], tag));
       if (__all(all)) break;
       if (++spins > kSpinLimit) {
         __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -179,7 +196,7 @@ __device__ __forceinline__ bool poll_k(int nw, uint32_t ep, uint32_t *err, int t
 #pragma unroll
     for (int k = 0; k < K; k++) {
       const int i = base + t + k * kPollThreads;
-      if (i < nw) put(i, w[k]);
+      if (i < nw) put(i, xword_vals(w[k]));
     }
   }
   return true;

@@ -756,6 +756,9 @@ itts_status check_persist(itts_kv *kv) {
   if (err == 0) return ITTS_OK;
   HIP_TRY(hipMemsetAsync(kv->xch.p, 0, kv->xch.bytes, s));
   HIP_TRY(hipMemsetAsync(kv->sync.p, 0, kv->sync.bytes, s));
+  // epochs restart with the cleared words (an exchange word keeps 16 epoch bits, so a
+  // cleared word must never meet an epoch that is 0 in those bits)
+  HIP_TRY(hipMemsetAsync(static_cast<char *>(kv->ctl.p) + offsetof(DecodeCtl, xstep), 0, sizeof(int32_t), s));
   HIP_TRY(hipStreamSynchronize(s));
   return set_error(ITTS_E_DEVICE, "decode step: a persistent-kernel exchange wait timed out");
 }

@@ -11,6 +11,8 @@ with the oracle's logits, within the workload's 2e-2 bar:
 
 - long utterance: 32 cond + 200 text, 1500 sampled steps (T 0.8, top-k 30, top-p 0.8,
   penalty 10, STOP masked), bf16 and fp32 caches, contexts to 1734 keys;
+- long greedy: 32 cond + 200 text, 1500 greedy steps (penalty 10) on the reference's fp32
+  cache, id for id against the oracle's free-running decode;
 - 4-bit weights: 32 + 128 text, 1500 greedy steps, contexts to 1662 keys;
 - short: 32 + 64 text, 128 greedy steps: identical ids with fp32 caches;
 - batch 8: text lengths U[20,200], decode lengths U[200,1200], sampled, bf16 caches,
@@ -151,6 +153,55 @@ def test_short_greedy_identical_f32(full_model, path):
     ref, _, _ = M.generate_codes_after(M.kv(2048, kv_bf16=False), pr.text_tokens, pr.conds, pr.lang_id, sp, st0,
                                        min_codes=128)
     assert codes.tolist() == ref.tolist()
+
+
+def _margin(row, seen_codes, params):
+    """Top-2 margin of the penalised logits the greedy pick sees (sampler.rs:138-157,
+    STOP masked): the perturbation that would swap the two best ids."""
+    x = np.array(row, dtype=np.float64, copy=True)
+    x[STOP] = -np.inf
+    p = float(params.repetition_penalty)
+    seen = np.unique(np.concatenate([np.asarray(seen_codes, np.int64), [1, 8192]]))
+    seen = seen[seen < len(x)]
+    x[seen] = np.where(x[seen] < 0, x[seen] * p, x[seen] / p)
+    top = np.sort(x)[-2:]
+    return float(top[1] - top[0])
+
+
+def test_long_greedy_identical_f32(full_model):
+    """The long prompt (32 cond + 200 text) with 1500 greedy steps (penalty 10, STOP
+    masked) on the reference's fp32 cache (gpt.rs:117,185-186), compared id for id with the
+    oracle's free-running generate_codes_after (the CP-11 semantics of sampler.rs:487-536
+    over the whole decode).  Should the ids part, the first departing step must be a
+    near-tie: its top-2 margin within 4x the logit difference the persistent step shows
+    at that context."""
+    W, g, M = full_model
+    say("[gpu] long 32+200, 1500 greedy steps, f32 cache, id for id against the oracle")
+    pr = synth.make_prompt(W.cfg, 32, 200, seed=2)
+    sp, st0, st_end, codes, kv = _generate(g, pr, 1500, GREEDY, H.ITTS_F32, 0)
+    assert kv.decode_path() == H.ITTS_DECODE_PERSISTENT
+    ref, _, _ = M.generate_codes_after(M.kv(2048, kv_bf16=False), pr.text_tokens, pr.conds, pr.lang_id, sp, st0,
+                                       min_codes=1500)
+    assert len(ref) == 1500
+    diff = np.nonzero(codes != ref)[0]
+    if len(diff) == 0:
+        say("[gpu]   1500 greedy ids identical to the oracle's free-running decode")
+        return
+    i = int(diff[0])
+    okv = M.kv(2048, kv_bf16=False)
+    row = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id, np.asarray(ref[:i], np.int32))
+    # the persistent step's logits there (code j sits at Mel position j + 2, gpt.rs:618-625)
+    hkv = g.kv_cache(2048, H.ITTS_F32)
+    if i == 0:
+        hrow = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, hkv)
+    else:
+        g.prefill_after(pr.text_tokens, pr.conds, pr.lang_id, np.asarray(ref[: i - 1], np.int32), hkv)
+        hrow = g.step(hkv, int(ref[i - 1]), i + 1)
+    err = float(np.abs(hrow - row).max())
+    m = _margin(row, ref[:i], sp)
+    say(f"[gpu]   first departure at step {i} (of 1500): oracle {int(ref[i])}, HIP {int(codes[i])}; "
+        f"oracle top-2 margin {m:.3g}, HIP-vs-oracle logit difference there {err:.3g}")
+    assert m <= 4 * err, "the ids part where the oracle's decision is not a near-tie"
 
 
 def test_short_greedy_bf16(full_model):
