@@ -141,9 +141,18 @@ hipError_t launch_attn_flash(const float *q, int T, int base, const int *kstart,
 hipError_t launch_log_softmax_pick(const float *logits, int R, int V, const int *codes, float *out, hipStream_t s);
 
 // Prefill GEMM: y = x[M][K] . Wdeq^T + bias with the same epilogues as the GEMV.
+// A LayerNorm folded into the product that follows it (few-row products, K <= 2048,
+// K % 256 == 0): the product runs on gamma * x straight from the fp32 rows x [M][K] and its
+// epilogue applies each row's statistics, rstd (sum - mean G[n]) + c[n], with G = W gamma
+// and c = W beta + bias (launch_ln_fold), in place of sum + bias.
+struct FoldIn {
+  const float *x, *gamma, *G, *c;
+};
+
 struct GemmArgs {
   DevQL ql;
-  SplitAct x;       // [M][K]
+  SplitAct x;       // [M][K] (unused with fold.x)
+  FoldIn fold;      // fold.x set: the input is LayerNorm(x) by the fold above
   int M;
   float *y;         // [M][N] (store) or residual stream [M][N] (resid)
   SplitOut xo;      // gelu: the next GEMM's input [M][N] (N a multiple of 64)

@@ -525,10 +525,16 @@ constexpr int kFewRows = 8, kFewMaxGw = 2, kFewMaxSplits = 16;
 constexpr int kFewWaves = 8;                  // waves per block, a K group each
 constexpr int kFewEPT = 512 / (64 * kFewWaves);  // of a tile's 8 x 64 results, per thread
 
-template <int BITS, int PT, int EPI, int KVT>
+// With FOLD (a.fold, one group a wave), row c's activations are gamma * x read from the fp32
+// rows and split to hi/lo here, their group sums formed here, and wave w forms the mean and
+// rstd of row w (biased variance, eps 1e-5, over K/256 float4s a lane in registers) beside
+// the product; the epilogue takes rstd (sum - mean G[n]) + c[n].
+constexpr int kFoldQ = 8;  // float4s a lane of a row's statistics: K <= 2048
+template <int BITS, int PT, int EPI, int KVT, bool FOLD>
 __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN, int S, int gw) {
   __shared__ float red[kFewWaves][512];
   __shared__ float gel[kFewRows][65];
+  __shared__ float row_mu[kFewRows], row_rs[kFewRows];
   __shared__ uint32_t last_flag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, c = lane & 31;
   const int tn = blockIdx.x % nN, ks = blockIdx.x / nN;
@@ -543,6 +549,8 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
   using PRaw = typename std::conditional<PT == kParamF16, uint32_t, float2>::type;
   PRaw pr[kFewMaxGw][2];
   float gsr[kFewMaxGw][4];       // group sums of the lane's live rows 4h + e
+  float4 xf[2][4];               // FOLD: row c, K 64 g + 32 kp + 16 h + 4 q .. +3 (gamma * x)
+  float4 st[kFoldQ];             // FOLD: row `wave`, float4s lane + 64 i
 #pragma unroll
   for (int gi = 0; gi < kFewMaxGw; gi++) {
     const int g = ks * kFewWaves * gw + kFewWaves * gi + wave;
@@ -553,7 +561,18 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       for (int kp = 0; kp < 2; kp++)
 #pragma unroll
         for (int q = 0; q < 2; q++) xa[gi][p2][kp][q] = u32x4{0u, 0u, 0u, 0u};
-    if (live && c < M) {
+    if constexpr (FOLD) {
+      if (gi == 0) {
+#pragma unroll
+        for (int kp = 0; kp < 2; kp++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int k = g * kGroup + 32 * kp + 16 * h + 4 * q;
+            xf[kp][q] = live && c < M ? reinterpret_cast<const float4 *>(a.fold.x + (size_t)c * K)[k >> 2]
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          }
+      }
+    } else if (live && c < M) {
       const size_t off = (size_t)c * K + (size_t)g * kGroup + 16 * h;
 #pragma unroll
       for (int kp = 0; kp < 2; kp++) {
@@ -584,10 +603,54 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       }
       pr[gi][j] = static_cast<const PRaw *>(a.ql.params)[(size_t)n * G + gl];
     }
+    if constexpr (!FOLD) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int m = 4 * h + e;
-      gsr[gi][e] = live && m < M ? a.x.gs[(size_t)m * G + g] : 0.0f;
+      for (int e = 0; e < 4; e++) {
+        const int m = 4 * h + e;
+        gsr[gi][e] = live && m < M ? a.x.gs[(size_t)m * G + g] : 0.0f;
+      }
+    }
+  }
+  if constexpr (FOLD) {
+    // gamma * x as hi/lo fp16 and the lane's share of row c's group sum (the other 32
+    // values are in lane c ^ 32)
+    const int g = ks * kFewWaves * gw + wave;
+    if (g < G) {
+      float gsum = 0.0f;
+#pragma unroll
+      for (int kp = 0; kp < 2; kp++)
+#pragma unroll
+        for (int sub = 0; sub < 2; sub++) {
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int q2 = 0; q2 < 2; q2++) {
+            const int k = g * kGroup + 32 * kp + 16 * h + 8 * sub + 4 * q2;
+            const float4 gm = reinterpret_cast<const float4 *>(a.fold.gamma)[k >> 2];
+            const float4 v = xf[kp][2 * sub + q2];
+            const float y[4] = {v.x * gm.x, v.y * gm.y, v.z * gm.z, v.w * gm.w};
+#pragma unroll
+            for (int e2 = 0; e2 < 2; e2++) {
+              gsum += y[2 * e2] + y[2 * e2 + 1];
+              uint32_t h0, l0, h1, l1;
+              split_f16(y[2 * e2], h0, l0);
+              split_f16(y[2 * e2 + 1], h1, l1);
+              hw[2 * q2 + e2] = h0 | (h1 << 16);
+              lw[2 * q2 + e2] = l0 | (l1 << 16);
+            }
+          }
+          xa[0][0][kp][sub] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+          xa[0][1][kp][sub] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        }
+      gsum += __shfl_xor(gsum, 32, 64);
+#pragma unroll
+      for (int e = 0; e < 4; e++) gsr[0][e] = __shfl(gsum, 4 * h + e, 64);
+    }
+    // this wave's row of the statistics
+#pragma unroll
+    for (int i = 0; i < kFoldQ; i++) {
+      const int q = lane + 64 * i;
+      st[i] = wave < M && q < (K >> 2) ? reinterpret_cast<const float4 *>(a.fold.x + (size_t)wave * K)[q]
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   }
 #pragma unroll
@@ -629,6 +692,27 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       if constexpr (BITS == 4) sb.y = sb.y - 16.0f * sb.x;
 #pragma unroll
       for (int e = 0; e < 4; e++) acc[j][e] = fmaf(sb.x, P[j][e], fmaf(sb.y, gsr[gi][e], acc[j][e]));
+    }
+  }
+  if constexpr (FOLD) {
+    if (wave < M) {  // wave-uniform
+      float s1 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kFoldQ; i++) s1 += (st[i].x + st[i].y) + (st[i].z + st[i].w);
+      const float mean = wave64_sum_dpp(s1) / (float)K;
+      float q2 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kFoldQ; i++) {
+        if (lane + 64 * i < (K >> 2)) {
+          const float d0 = st[i].x - mean, d1 = st[i].y - mean, d2 = st[i].z - mean, d3 = st[i].w - mean;
+          q2 += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+      }
+      const float rstd = 1.0f / sqrtf(wave64_sum_dpp(q2) / (float)K + 1e-5f);
+      if (lane == 0) {
+        row_mu[wave] = mean;
+        row_rs[wave] = rstd;
+      }
     }
   }
   // the waves' partials, added in wave order: entry i = (j, e, lane)
@@ -683,7 +767,8 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
     for (int q = 0; q < kFewEPT; q++) {
       const int i = tid + 64 * kFewWaves * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
       const int m = 4 * (ln >> 5) + e, cl = 32 * j + (ln & 31), n = n0 + cl;
-      const float gv = gelu_tanh(v[q] + a.ql.bias[n]);  // N is a multiple of 64 here
+      const float gv = gelu_tanh(FOLD && m < M ? row_rs[m] * (v[q] - row_mu[m] * a.fold.G[n]) + a.fold.c[n]
+                                              : v[q] + a.ql.bias[n]);  // N is a multiple of 64 here
       gel[m][cl] = gv;
       if (m < M) {
         uint32_t hb, lb;
@@ -707,7 +792,7 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       const int i = tid + 64 * kFewWaves * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
       const int m = 4 * (ln >> 5) + e, n = n0 + 32 * j + (ln & 31);
       if (m >= M || n >= N) continue;
-      const float val = v[q] + a.ql.bias[n];
+      const float val = FOLD ? row_rs[m] * (v[q] - row_mu[m] * a.fold.G[n]) + a.fold.c[n] : v[q] + a.ql.bias[n];
       if constexpr (EPI == kEpiStore) {
         a.y[(size_t)m * N + n] = val;
       } else if constexpr (EPI == kEpiResid) {
@@ -892,9 +977,10 @@ hipError_t gemm_dispatch(const GemmArgs &a, const Plan &p, int epi, int kvt, hip
   }
 }
 
-template <int BITS, int PT, int EPI, int KVT>
+template <int BITS, int PT, int EPI, int KVT, bool FOLD = false>
 hipError_t few_launch(const GemmArgs &a, int nN, int S, int gw, hipStream_t s) {
-  hipLaunchKernelGGL((few_kernel<BITS, PT, EPI, KVT>), dim3(nN * S), dim3(64 * kFewWaves), 0, s, a, nN, S, gw);
+  hipLaunchKernelGGL((few_kernel<BITS, PT, EPI, KVT, FOLD>), dim3(nN * S), dim3(64 * kFewWaves), 0, s, a, nN, S,
+                     gw);
   return hipGetLastError();
 }
 
@@ -906,8 +992,12 @@ hipError_t few_dispatch(const GemmArgs &a, int nN, int S, int gw, int epi, int k
     case kEpiResid:
       return few_launch<BITS, PT, kEpiResid, 0>(a, nN, S, gw, s);
     case kEpiGelu:
-      return few_launch<BITS, PT, kEpiGelu, 0>(a, nN, S, gw, s);
+      return a.fold.x ? few_launch<BITS, PT, kEpiGelu, 0, true>(a, nN, S, gw, s)
+                      : few_launch<BITS, PT, kEpiGelu, 0>(a, nN, S, gw, s);
     case kEpiQKV:
+      if (a.fold.x)
+        return kvt == kKvBf16 ? few_launch<BITS, PT, kEpiQKV, kKvBf16, true>(a, nN, S, gw, s)
+                              : few_launch<BITS, PT, kEpiQKV, kKvF32, true>(a, nN, S, gw, s);
       return kvt == kKvBf16 ? few_launch<BITS, PT, kEpiQKV, kKvBf16>(a, nN, S, gw, s)
                             : few_launch<BITS, PT, kEpiQKV, kKvF32>(a, nN, S, gw, s);
     default:
@@ -933,12 +1023,18 @@ size_t gemm_ws_floats(int n_cu) {
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s) {
   if (a.ql.K % kGroup != 0 || a.M <= 0 || a.ql.N <= 0) return hipErrorInvalidValue;
   if (epi == kEpiGelu && a.ql.N % kGroup != 0) return hipErrorInvalidValue;
+  if (a.fold.x) {  // the folded LayerNorm: few-row products with one group a wave only
+    if (a.M > kFewRows || (bits != 8 && bits != 4) || a.ql.K % 256 != 0 || a.ql.K > 256 * kFoldQ ||
+        (epi != kEpiQKV && epi != kEpiGelu) || !a.fold.gamma || !a.fold.G || !a.fold.c)
+      return hipErrorInvalidValue;
+  }
   if (a.M <= kFewRows && (bits == 8 || bits == 4)) {
     // a group per wave while that keeps the splits within kFewMaxSplits, else two
     const int nN = (a.ql.N + 63) / 64, G = a.ql.K / kGroup;
     const int gw = (G + kFewWaves * kFewMaxSplits - 1) / (kFewWaves * kFewMaxSplits);
     const int S = (G + kFewWaves * gw - 1) / (kFewWaves * gw);
     const bool ws_ok = S == 1 || (a.ws && a.cnt && (size_t)nN * S * 512 <= a.ws_floats && nN <= a.cnt_words);
+    if (a.fold.x && (!ws_ok || gw != 1)) return hipErrorInvalidValue;
     if (ws_ok && gw <= kFewMaxGw) {
       if (bits == 8)
         return ptype == kParamF16 ? few_dispatch<8, kParamF16>(a, nN, S, gw, epi, kvt, s)

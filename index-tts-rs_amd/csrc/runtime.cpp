@@ -142,8 +142,9 @@ struct itts_gpt {
   std::vector<DevLayer> layers;
   DevBuf ln_f_w, ln_f_b, fn_w, fn_b;
   DevQL head{};
-  // persistent decode step: device copy of `layers`, the folded LayerNorm rows
-  // (fold_floats(d, F) per layer), blocks (one per compute unit)
+  // persistent decode step: device copy of `layers`; the folded LayerNorm rows
+  // (fold_floats(d, F) per layer, int8 and int4 codes; the batched step's products use
+  // them too); blocks (one per compute unit)
   DevBuf dlayers, fold;
   int n_cu = 0;
   int device = 0;
@@ -707,10 +708,18 @@ itts_status enqueue_step_batch(itts_gpt *g, int B, int max_seq, int kvt) {
   float *X = g->bx.as<float>();
   HIP_TRY(launch_embed_batch(seqs, B, g->mel_emb.as<float>(), g->mel_pos.as<float>(), d, X, s));
   const size_t layer_elems = (size_t)c.n_head * max_seq * 64;
+  // ln_1 and ln_2 folded into the products that follow them (no row kernels) where the
+  // few-row products take them: up to 8 rows, d a multiple of 256 up to 2048
+  const bool fold = g->fold.p && B <= 8 && d % 256 == 0 && d <= 2048;
+  const size_t per = fold_floats(d, c.d_ffn);
   for (int l = 0; l < c.n_layer; l++) {
     const DevLayer &L = g->layers[l];
-    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, B, d, g->bh.out(), s));
+    const float *fo = fold ? g->fold.as<float>() + per * l : nullptr;
     GemmArgs ga = gemm_args(g, L.attn, g->bh.act(), B);
+    if (fold)
+      ga.fold = FoldIn{X, L.ln1_w, fo, fo + 3 * d};
+    else
+      HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, B, d, g->bh.out(), s));
     ga.qkv = QkvDst{g->bq.as<float>(), nullptr, nullptr, max_seq, 0, d, seqs, layer_elems * l};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kvt, s));
     HIP_TRY(launch_decode_batch_parts(g->bq.as<float>(), seqs, B, layer_elems * l, c.n_head, max_seq,
@@ -718,8 +727,11 @@ itts_status enqueue_step_batch(itts_gpt *g, int B, int max_seq, int kvt) {
     ga = gemm_args(g, L.proj, g->ba.act(), B);
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kvt, s));
-    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, B, d, g->bh.out(), s));
     ga = gemm_args(g, L.fc, g->bh.act(), B);
+    if (fold)
+      ga.fold = FoldIn{X, L.ln2_w, fo + 6 * d, fo + 6 * d + c.d_ffn};
+    else
+      HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, B, d, g->bh.out(), s));
     ga.xo = g->bf.out();
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kvt, s));
     ga = gemm_args(g, L.mproj, g->bf.act(), B);
@@ -982,7 +994,7 @@ itts_status itts_gpt_create(const itts_weights *w, itts_gpt **out) {
       return fail(set_error(ITTS_E_DEVICE, "device attribute query failed"));
     g->device = dev;
     g->persist_ok = (bits == 8 || bits == 4) && coop != 0 && persist_init() == hipSuccess;
-    if (g->persist_ok) {  // G and c of the products that follow ln_1 and ln_2
+    if (bits == 8 || bits == 4) {  // G and c of the products that follow ln_1 and ln_2
       const size_t per = fold_floats(d, F);
       if (g->fold.ensure(sizeof(float) * per * c.n_layer) != hipSuccess)
         return fail(set_error(ITTS_E_DEVICE, "fold buffer allocation failed"));
