@@ -267,56 +267,11 @@ hipError_t gemv_dispatch_pe(const GemvArgs &a, int pro, int epi, int kvt, hipStr
 }
 
 // ---------------------------------------------------------------------------------
-// Decode attention: grid (head, split), 256 keys per split (4 waves x 64 keys).  Each
-// block writes its partial (max, denominator, 64 unnormalised outputs); the c_proj GEMV
-// that consumes the attention output combines the partials in its prologue.
+// Decode attention: grid (head, split), 256 keys per split (4 waves x 64 keys, each wave
+// one tile of attn_range below).  Each block writes its partial (max, denominator, 64
+// unnormalised outputs); the c_proj GEMV that consumes the attention output combines the
+// partials in its prologue.
 // ---------------------------------------------------------------------------------
-
-template <int KVT>
-__device__ inline void load_row64(const void *base, size_t row, float *out) {
-  if constexpr (KVT == kKvBf16) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint4 u = p[i];
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        out[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
-        out[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-      }
-    }
-  } else {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + row * 64);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float4 f = p[i];
-      out[4 * i] = f.x;
-      out[4 * i + 1] = f.y;
-      out[4 * i + 2] = f.z;
-      out[4 * i + 3] = f.w;
-    }
-  }
-}
-
-// 8 consecutive elements of row `row` starting at column c0.
-template <int KVT>
-__device__ inline void load_row8(const void *base, size_t row, int c0, float *out) {
-  if constexpr (KVT == kKvBf16) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      out[2 * j] = __uint_as_float(w[j] << 16);
-      out[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-    }
-  } else {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(base) + row * 64 + c0);
-    const float4 f0 = p[0], f1 = p[1];
-    out[0] = f0.x; out[1] = f0.y; out[2] = f0.z; out[3] = f0.w;
-    out[4] = f1.x; out[5] = f1.y; out[6] = f1.z; out[7] = f1.w;
-  }
-}
 
 template <int KVT>
 __device__ inline const void *head_base(const void *c, size_t off) {
@@ -324,8 +279,120 @@ __device__ inline const void *head_base(const void *c, size_t off) {
                         : (const void *)(static_cast<const float *>(c) + off);
 }
 
+// Eight consecutive elements of a cache row, held in the cache dtype until used.
+template <int KVT>
+struct Row8 {
+  uint32_t w[KVT == kKvBf16 ? 4 : 8];
+  __device__ __forceinline__ void load(const void *base, size_t row, int c0) {
+    if constexpr (KVT == kKvBf16) {
+      const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
+      w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+    } else {
+      const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + row * 64 + c0);
+      const uint4 u0 = p[0], u1 = p[1];
+      w[0] = u0.x; w[1] = u0.y; w[2] = u0.z; w[3] = u0.w;
+      w[4] = u1.x; w[5] = u1.y; w[6] = u1.z; w[7] = u1.w;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < (KVT == kKvBf16 ? 4 : 8); i++) w[i] = 0u;
+  }
+  __device__ __forceinline__ float at(int e) const {
+    if constexpr (KVT == kKvBf16)
+      return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+    else
+      return __uint_as_float(w[e]);
+  }
+};
+
+// Score (q.k / 8) of key row `kr`, whose dims 8 dc .. 8 dc + 7 this lane holds against
+// q's in qa, qb: the lane's partial dot, summed over the key's eight lanes (xor 1, xor 2,
+// then the 8-lane mirror; both lanes of each pair form the same sum, so all eight lanes
+// hold one bit-identical score).  Every lane of the wave must be active.
+template <int KVT>
+__device__ __forceinline__ float row_score(const float4 &qa, const float4 &qb, const Row8<KVT> &kr) {
+  float t = qa.x * kr.at(0) + qa.y * kr.at(1) + qa.z * kr.at(2) + qa.w * kr.at(3) +
+            (qb.x * kr.at(4) + qb.y * kr.at(5) + qb.z * kr.at(6) + qb.w * kr.at(7));
+  t += dpp_pair<0xB1>(t);
+  t += dpp_pair<0x4E>(t);
+  t += dpp_pair<0x141>(t);
+  return t * 0.125f;
+}
+
+// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows), 64 keys
+// a tile.  Lane = (key group kg = lane / 8, dims 8 (lane % 8) .. +7): a lane holds keys
+// kg, kg + 8, .. of the tile, K and V rows both spread over eight adjacent lanes (16 bytes
+// each, so a load instruction reads eight whole rows) and all of a tile's loads are in
+// flight at once; probabilities stay in the lane that holds the key, and the eight key
+// groups are added once at the end.  o returns dimension `lane`.
+template <int KVT>
+__device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
+                                  float &m, float &l, float &o) {
+  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
+  const float4 qa = reinterpret_cast<const float4 *>(q)[2 * dc], qb = reinterpret_cast<const float4 *>(q)[2 * dc + 1];
+  m = -INFINITY;
+  l = 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+  for (int t0 = j0; t0 < j1; t0 += 64) {
+    Row8<KVT> kr[8], vr[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int key = t0 + kg + 8 * jj;
+      if (key < j1) {
+        kr[jj].load(kh, (size_t)key, dc * 8);
+        vr[jj].load(vh, (size_t)key, dc * 8);
+      } else {
+        kr[jj].zero();
+        vr[jj].zero();
+      }
+    }
+    float sc[8], mt = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const float v = row_score<KVT>(qa, qb, kr[jj]);
+      sc[jj] = t0 + kg + 8 * jj < j1 ? v : -INFINITY;
+      mt = fmaxf(mt, sc[jj]);
+    }
+    mt = wave64_max_dpp(mt);
+    const float mn = fmaxf(m, mt);
+    const float corr = (m == -INFINITY) ? 0.0f : __expf(m - mn);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] *= corr;
+    float ps = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const float p = t0 + kg + 8 * jj < j1 ? __expf(sc[jj] - mn) : 0.0f;
+      ps += p;
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] += p * vr[jj].at(e);
+    }
+    // the tile's probability sum over the eight key groups (lane ^ 8, ^ 16, ^ 32)
+    ps += dpp_pair<0x128>(ps);
+    ps += swizzle_xor16(ps);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * corr + ps;
+    m = mn;
+  }
+  // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits in
+  // element lane % 8 of lane lane / 8
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    acc[e] += dpp_pair<0x128>(acc[e]);  // row_ror:8 = lane ^ 8
+    acc[e] += swizzle_xor16(acc[e]);
+    acc[e] += __shfl_xor(acc[e], 32, 64);
+  }
+  o = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = __shfl(acc[e], lane >> 3, 64);
+    if (dc == e) o = x;
+  }
+}
+
 struct AttnShared {
-  float p[4][64];      // probabilities per wave
   float o[4][64];      // per-wave unnormalised outputs
   float m[4], l[4];
 };
@@ -341,63 +408,10 @@ __device__ inline void attn_decode_block(const float *q, const void *kc, const v
   if (s >= S) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const size_t hb = (size_t)h * max_seq * 64;
-  const void *kh = head_base<KVT>(kc, hb);
-  const void *vh = head_base<KVT>(vc, hb);
-  const int jw = s * kAttnKeys + wave * 64;  // this wave's first key
-  const int j = jw + lane;
-  const int kg = lane >> 3, dg = lane & 7;   // P.V layout: key group, 8-wide dim group
-
-  // K row of this lane's key and the V slices of its P.V share, all loads in flight at once
-  float kr[64];
-  if (j < L) load_row64<KVT>(kh, (size_t)j, kr);
-  float v8[8][8];
-#pragma unroll
-  for (int kk = 0; kk < 8; kk++) {
-    const int key = jw + kg + 8 * kk;
-    if (key < L) {
-      load_row8<KVT>(vh, (size_t)key, dg * 8, v8[kk]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; e++) v8[kk][e] = 0.0f;
-    }
-  }
-  float sc = -INFINITY;
-  if (j < L) {
-    const float4 *q4 = reinterpret_cast<const float4 *>(q + h * 64);
-    float dot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float4 qv = q4[i];
-      dot += qv.x * kr[4 * i] + qv.y * kr[4 * i + 1] + qv.z * kr[4 * i + 2] + qv.w * kr[4 * i + 3];
-    }
-    sc = dot * 0.125f;
-  }
-  const float mw = wave64_max_dpp(sc);
-  const float p = (j < L) ? __expf(sc - mw) : 0.0f;
-  const float lw = wave64_sum_dpp(p);
-  sh.p[wave][lane] = p;
-  __syncthreads();
-  float o8[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) o8[e] = 0.0f;
-#pragma unroll
-  for (int kk = 0; kk < 8; kk++) {
-    const float pk = sh.p[wave][kg + 8 * kk];
-#pragma unroll
-    for (int e = 0; e < 8; e++) o8[e] += pk * v8[kk][e];
-  }
-  // add the key groups (lanes dg, dg + 8, .., dg + 56): lane ^ 8 by DPP (row_ror:8), lane ^ 16
-  // by swizzle, lane ^ 32 by one permute
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    o8[e] += dpp_pair<0x128>(o8[e]);
-    o8[e] += swizzle_xor16(o8[e]);
-    o8[e] += __shfl_xor(o8[e], 32, 64);
-  }
-  if (kg == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) sh.o[wave][dg * 8 + e] = o8[e];
-  }
+  const int jw = s * kAttnKeys + wave * 64;  // this wave's 64 keys (one tile of attn_range)
+  float mw, lw, o;
+  attn_range<KVT>(q + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), jw, min(jw + 64, L), mw, lw, o);
+  sh.o[wave][lane] = o;
   if (lane == 0) {
     sh.m[wave] = mw;
     sh.l[wave] = lw;
@@ -532,119 +546,6 @@ __global__ __launch_bounds__(256) void embed_batch_kernel(const BatchSeq *seqs, 
 __global__ void advance_batch_kernel(const BatchSeq *seqs, int B) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b < B && !seqs[b].ctl->done) seqs[b].ctl->valid_len += 1;
-}
-
-// Eight consecutive elements of a cache row, held in the cache dtype until used.
-template <int KVT>
-struct Row8 {
-  uint32_t w[KVT == kKvBf16 ? 4 : 8];
-  __device__ __forceinline__ void load(const void *base, size_t row, int c0) {
-    if constexpr (KVT == kKvBf16) {
-      const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
-      w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
-    } else {
-      const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + row * 64 + c0);
-      const uint4 u0 = p[0], u1 = p[1];
-      w[0] = u0.x; w[1] = u0.y; w[2] = u0.z; w[3] = u0.w;
-      w[4] = u1.x; w[5] = u1.y; w[6] = u1.z; w[7] = u1.w;
-    }
-  }
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int i = 0; i < (KVT == kKvBf16 ? 4 : 8); i++) w[i] = 0u;
-  }
-  __device__ __forceinline__ float at(int e) const {
-    if constexpr (KVT == kKvBf16)
-      return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
-    else
-      return __uint_as_float(w[e]);
-  }
-};
-
-// Score (q.k / 8) of key row `kr`, whose dims 8 dc .. 8 dc + 7 this lane holds against
-// q's in qa, qb: the lane's partial dot, summed over the key's eight lanes (xor 1, xor 2,
-// then the 8-lane mirror; both lanes of each pair form the same sum, so all eight lanes
-// hold one bit-identical score).  Every lane of the wave must be active.
-template <int KVT>
-__device__ __forceinline__ float row_score(const float4 &qa, const float4 &qb, const Row8<KVT> &kr) {
-  float t = qa.x * kr.at(0) + qa.y * kr.at(1) + qa.z * kr.at(2) + qa.w * kr.at(3) +
-            (qb.x * kr.at(4) + qb.y * kr.at(5) + qb.z * kr.at(6) + qb.w * kr.at(7));
-  t += dpp_pair<0xB1>(t);
-  t += dpp_pair<0x4E>(t);
-  t += dpp_pair<0x141>(t);
-  return t * 0.125f;
-}
-
-// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows), 64 keys
-// a tile.  Lane = (key group kg = lane / 8, dims 8 (lane % 8) .. +7): a lane holds keys
-// kg, kg + 8, .. of the tile, K and V rows both spread over eight adjacent lanes (16 bytes
-// each, so a load instruction reads eight whole rows) and all of a tile's loads are in
-// flight at once; probabilities stay in the lane that holds the key, and the eight key
-// groups are added once at the end.  o returns dimension `lane`.
-template <int KVT>
-__device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
-                                  float &m, float &l, float &o) {
-  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
-  const float4 qa = reinterpret_cast<const float4 *>(q)[2 * dc], qb = reinterpret_cast<const float4 *>(q)[2 * dc + 1];
-  m = -INFINITY;
-  l = 0.0f;
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-  for (int t0 = j0; t0 < j1; t0 += 64) {
-    Row8<KVT> kr[8], vr[8];
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const int key = t0 + kg + 8 * jj;
-      if (key < j1) {
-        kr[jj].load(kh, (size_t)key, dc * 8);
-        vr[jj].load(vh, (size_t)key, dc * 8);
-      } else {
-        kr[jj].zero();
-        vr[jj].zero();
-      }
-    }
-    float sc[8], mt = -INFINITY;
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const float v = row_score<KVT>(qa, qb, kr[jj]);
-      sc[jj] = t0 + kg + 8 * jj < j1 ? v : -INFINITY;
-      mt = fmaxf(mt, sc[jj]);
-    }
-    mt = wave64_max_dpp(mt);
-    const float mn = fmaxf(m, mt);
-    const float corr = (m == -INFINITY) ? 0.0f : __expf(m - mn);
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] *= corr;
-    float ps = 0.0f;
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const float p = t0 + kg + 8 * jj < j1 ? __expf(sc[jj] - mn) : 0.0f;
-      ps += p;
-#pragma unroll
-      for (int e = 0; e < 8; e++) acc[e] += p * vr[jj].at(e);
-    }
-    // the tile's probability sum over the eight key groups (lane ^ 8, ^ 16, ^ 32)
-    ps += dpp_pair<0x128>(ps);
-    ps += swizzle_xor16(ps);
-    ps += __shfl_xor(ps, 32, 64);
-    l = l * corr + ps;
-    m = mn;
-  }
-  // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits in
-  // element lane % 8 of lane lane / 8
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    acc[e] += dpp_pair<0x128>(acc[e]);  // row_ror:8 = lane ^ 8
-    acc[e] += swizzle_xor16(acc[e]);
-    acc[e] += __shfl_xor(acc[e], 32, 64);
-  }
-  o = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float x = __shfl(acc[e], lane >> 3, 64);
-    if (dc == e) o = x;
-  }
 }
 
 // Stores one fp32 value of a row in the GEMM's split form; the wave's 64 lanes hold one
