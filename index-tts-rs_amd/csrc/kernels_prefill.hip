@@ -540,6 +540,21 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
   const int tn = blockIdx.x % nN, ks = blockIdx.x / nN;
   const int N = a.ql.N, K = a.ql.K, G = K / kGroup, M = a.M;
   const int n0 = tn * 64;
+  // the epilogue's operands of this thread's results (entry i = tid + 512 q -> row
+  // m = 4 (i & 63) / 32 + (i >> 6) % 4, column n0 + 32 (i >> 8) + i % 32), loaded first so
+  // that their latency passes during the product; only the tile's last block uses them
+  float ep_b[kFewEPT], ep_g[kFewEPT], ep_y[kFewEPT];
+  BatchSeq ep_sq[kFewEPT];
+#pragma unroll
+  for (int q = 0; q < kFewEPT; q++) {
+    const int i = tid + 64 * kFewWaves * q, ln = i & 63;
+    const int m = 4 * (ln >> 5) + ((i >> 6) & 3), n = min(n0 + 32 * (i >> 8) + (ln & 31), N - 1);
+    ep_b[q] = FOLD ? a.fold.c[n] : a.ql.bias[n];
+    ep_g[q] = FOLD ? a.fold.G[n] : 0.0f;
+    ep_y[q] = EPI == kEpiResid && m < M ? a.y[(size_t)m * N + n] : 0.0f;
+    if constexpr (EPI == kEpiQKV)
+      if (a.qkv.seqs) ep_sq[q] = a.qkv.seqs[min(m, M - 1)];
+  }
   // this wave's groups: ks * 4 gw + 4 i + wave, i < gw (none past G)
   floatx4 acc[2] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}, floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
   u32x4 xa[kFewMaxGw][2][2][2];  // [group][plane][kp][half]: row c, K 32 kp + 16 h .. +15
@@ -694,8 +709,20 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       for (int e = 0; e < 4; e++) acc[j][e] = fmaf(sb.x, P[j][e], fmaf(sb.y, gsr[gi][e], acc[j][e]));
     }
   }
+  // a batched QKV row's cache position and state (the sequence's control block)
+  int ep_pos[kFewEPT], ep_done[kFewEPT];
+#pragma unroll
+  for (int q = 0; q < kFewEPT; q++) {
+    ep_pos[q] = 0;
+    ep_done[q] = 0;
+    if constexpr (EPI == kEpiQKV)
+      if (a.qkv.seqs) {
+        ep_pos[q] = ep_sq[q].ctl->valid_len;
+        ep_done[q] = ep_sq[q].ctl->done;
+      }
+  }
   if constexpr (FOLD) {
-    if (wave < M) {  // wave-uniform
+    {  // rows past M have zero statistics' inputs (mean 0); their results are not stored
       float s1 = 0.0f;
 #pragma unroll
       for (int i = 0; i < kFoldQ; i++) s1 += (st[i].x + st[i].y) + (st[i].z + st[i].w);
@@ -767,8 +794,8 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
     for (int q = 0; q < kFewEPT; q++) {
       const int i = tid + 64 * kFewWaves * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
       const int m = 4 * (ln >> 5) + e, cl = 32 * j + (ln & 31), n = n0 + cl;
-      const float gv = gelu_tanh(FOLD && m < M ? row_rs[m] * (v[q] - row_mu[m] * a.fold.G[n]) + a.fold.c[n]
-                                              : v[q] + a.ql.bias[n]);  // N is a multiple of 64 here
+      const float gv = gelu_tanh(FOLD ? row_rs[m] * (v[q] - row_mu[m] * ep_g[q]) + ep_b[q]
+                                      : v[q] + ep_b[q]);  // N is a multiple of 64 here
       gel[m][cl] = gv;
       if (m < M) {
         uint32_t hb, lb;
@@ -792,11 +819,11 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
       const int i = tid + 64 * kFewWaves * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
       const int m = 4 * (ln >> 5) + e, n = n0 + 32 * j + (ln & 31);
       if (m >= M || n >= N) continue;
-      const float val = FOLD ? row_rs[m] * (v[q] - row_mu[m] * a.fold.G[n]) + a.fold.c[n] : v[q] + a.ql.bias[n];
+      const float val = FOLD ? row_rs[m] * (v[q] - row_mu[m] * ep_g[q]) + ep_b[q] : v[q] + ep_b[q];
       if constexpr (EPI == kEpiStore) {
         a.y[(size_t)m * N + n] = val;
       } else if constexpr (EPI == kEpiResid) {
-        a.y[(size_t)m * N + n] += val;
+        a.y[(size_t)m * N + n] = ep_y[q] + val;
       } else {
         const int d = a.qkv.d_model;
         if (n < d) {
@@ -807,10 +834,10 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
           void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
           int pos = a.qkv.pos0 + m;
           if (a.qkv.seqs) {  // batched decode: row m is sequence m
-            const BatchSeq &sq = a.qkv.seqs[m];
-            if (sq.ctl->done) continue;
-            pos = sq.ctl->valid_len;
-            cache = static_cast<char *>(n < 2 * d ? sq.k : sq.v) + a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4);
+            if (ep_done[q]) continue;
+            pos = ep_pos[q];
+            cache = static_cast<char *>(n < 2 * d ? ep_sq[q].k : ep_sq[q].v) +
+                    a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4);
           }
           const size_t ci = ((size_t)hh * a.qkv.max_seq + pos) * kHeadDim + e2;
           if constexpr (KVT == kKvBf16) {
