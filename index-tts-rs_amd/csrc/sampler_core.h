@@ -13,9 +13,12 @@
 // Stages: (1) each thread holds up to 9 consecutive logits in registers, applies the
 // STOP mask and the repetition penalty; (2) greedy: block argmax; (3) otherwise scale by
 // 1/T, radix-select the k-th largest key (4 passes of 8 bits over an order-preserving
-// 32-bit key), take ties at the threshold by lowest index (block prefix scan), sort the k
-// candidates (one wave in registers for k <= 64, else a block-wide bitonic network in
-// LDS); (4) one thread forms the probabilities' prefix sums, the top-p cut and the draw.
+// 32-bit key; the first pass, which counts every key into few bins, spreads its LDS
+// atomics over 16 padded histogram copies), take ties at the threshold by lowest index
+// (block prefix scan), sort the k candidates (one wave in registers for k <= 64, else a
+// block-wide bitonic network in LDS); (4) the probabilities' sequential prefix sums, the
+// top-p cut and the draw: for k <= 64 by the sorting wave in registers (uniform loops of
+// single adds over values read lane by lane), else by one thread over LDS.
 #pragma once
 
 #include "common.h"
@@ -24,6 +27,7 @@ namespace itts {
 
 constexpr int kSampThreads = 1024;
 constexpr int kSampPerThread = 9;  // n <= 9216
+constexpr int kHistCopies = 16, kHistStride = 257;  // radix pass 0's histogram copies
 
 // Every multiply and add below rounds on its own (no FMA contraction), as the reference's
 // scalar Rust code does; the exponential uses explicit fmaf where intended.
@@ -73,13 +77,64 @@ __device__ inline float key_value(uint32_t k) {
 }
 
 struct SamplerShared {  // the sampler's LDS scratch (besides the sort keys)
-  uint32_t hist[256];
+  uint32_t hist[kHistCopies * kHistStride];
   int32_t wave_tot[kSampThreads / 64];
   int32_t scal[8];
   float fred[kSampThreads / 64];
   int32_t ired[kSampThreads / 64];
 };
 
+
+__device__ __forceinline__ float lane_f(float v, int i) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+// Stage (4) for k <= 64 candidates held by one wave, sorted (lane i: candidate i, key
+// (order key << 32 | ~id), lanes >= k zero): p_i = exp(v_i - v_0), the sequential fp32
+// sums S_i = p_0 + .. + p_i (left to right, one add at a time, as the reference's loops
+// run), the top-p cut over the normalised p_i / S_{k-1} (cumulated in the same order), and
+// the draw u * S_{active-1} against S_0, S_1, ..  Each loop over i is a uniform loop of
+// single adds on values read from lane i, so every sum is the serial one, bit for bit.
+__device__ inline int32_t sample_sorted_wave(uint64_t x, int k, const DevSampling &p, uint64_t *rng) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const uint32_t kx = (uint32_t)(x >> 32);
+  const int32_t id = (int32_t)(0xffffffffu - (uint32_t)x);
+  const float v0 = key_value((uint32_t)__builtin_amdgcn_readlane((int)kx, 0));
+  const float mx = is_finite(v0) ? v0 : 0.0f;
+  const float vi = key_value(kx);
+  const float pi = lane < k && is_finite(vi) ? sampler_expf(sub_rn(vi, mx)) : 0.0f;
+  float s = 0.0f, S = 0.0f;
+  for (int i = 0; i < k; i++) {
+    s = add_rn(s, lane_f(pi, i));
+    if (lane == i) S = s;
+  }
+  const float prob_sum = s;
+  int32_t tok = __builtin_amdgcn_readlane(id, 0);
+  if (prob_sum > 0.0f && is_finite(prob_sum)) {
+    const float norm = div_rn(pi, prob_sum);
+    float cum = 0.0f;
+    int active = k;
+    for (int i = 0; i < k; i++) {
+      if (i > 0 && cum > p.top_p) {
+        active = i;
+        break;
+      }
+      cum = add_rn(cum, lane_f(norm, i));
+    }
+    const float active_sum = lane_f(S, active - 1);
+    if (active_sum > 0.0f && is_finite(active_sum)) {
+      uint32_t upper = 0;
+      if (lane == 0) upper = (uint32_t)(splitmix_next(rng) >> 40);
+      upper = (uint32_t)__builtin_amdgcn_readlane((int)upper, 0);
+      const float u = mul_rn((float)upper, 1.0f / 16777216.0f);
+      const float draw = mul_rn(u, active_sum);
+      const uint64_t hit = __ballot(lane < active && draw <= S);
+      tok = __builtin_amdgcn_readlane(id, hit ? (int)__builtin_ctzll(hit) : active - 1);
+    }
+  }
+  return tok;
+}
 
 // The token sample_next_token returns for logits src[0..n) (read only; LDS or global), run
 // by all kSampThreads threads of the block, which all get the result.  seen: the penalty
@@ -178,12 +233,17 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
     int remaining = k;
     for (int pass = 0; pass < 4; pass++) {
       const int shift = 24 - 8 * pass;
-      for (int b = tid; b < 256; b += kSampThreads) sh.hist[b] = 0;
+      // pass 0 counts every key, whose top byte (sign and exponent) takes few values: the
+      // counts go to kHistCopies copies (by lane), padded apart so that lanes with one bin
+      // hit distinct LDS banks; later passes count few keys, into copy 0
+      const int copies = pass == 0 ? kHistCopies : 1;
+      for (int b = tid; b < copies * kHistStride; b += kSampThreads) sh.hist[b] = 0;
       __syncthreads();
+      uint32_t *hcopy = sh.hist + (pass == 0 ? (lane % kHistCopies) * kHistStride : 0);
 #pragma unroll
       for (int e = 0; e < kSampPerThread; e++) {
         const int i = i0 + e;
-        if (e < E && i < n && (key[e] & pmask) == prefix) atomicAdd(&sh.hist[(key[e] >> shift) & 255u], 1u);
+        if (e < E && i < n && (key[e] & pmask) == prefix) atomicAdd(&hcopy[(key[e] >> shift) & 255u], 1u);
       }
       __syncthreads();
       if (wave == 0) {
@@ -192,7 +252,8 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
         uint32_t tot = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          c[j] = sh.hist[255 - 4 * lane - j];
+          c[j] = 0;
+          for (int cp = 0; cp < copies; cp++) c[j] += sh.hist[cp * kHistStride + 255 - 4 * lane - j];
           tot += c[j];
         }
         uint32_t incl = tot;
@@ -257,7 +318,8 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
     __syncthreads();
     if (P <= 64) {
       // one wave sorts the candidates in registers (bitonic network over lane pairs, descending;
-      // keys are distinct, so the order equals the block-wide network's)
+      // keys are distinct, so the order equals the block-wide network's), then forms the
+      // probabilities, their sequential sums, the top-p cut and the draw in registers
       if (wave == 0) {
         uint64_t x = lane < k ? sk[lane] : 0ull;
         for (int size = 2; size <= 64; size <<= 1)
@@ -268,27 +330,28 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
             const bool keep_max = ((lane & size) == 0) == ((lane & stride) == 0);
             x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
           }
-        if (lane < k) sk[lane] = x;
+        const int32_t tok = sample_sorted_wave(x, k, p, rng);
+        if (lane == 0) sh.scal[3] = tok;
       }
       __syncthreads();
-    } else {
-      for (int i = k + tid; i < P; i += kSampThreads) sk[i] = 0ull;
-      __syncthreads();
-      // bitonic sort, descending
-      for (int size = 2; size <= P; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          for (int t = tid; t < P / 2; t += kSampThreads) {
-            const int i = 2 * t - (t & (stride - 1));
-            const int j = i + stride;
-            const bool desc = (i & size) == 0;
-            const uint64_t x = sk[i], y = sk[j];
-            if ((x < y) == desc) {
-              sk[i] = y;
-              sk[j] = x;
-            }
+      return sh.scal[3];
+    }
+    for (int i = k + tid; i < P; i += kSampThreads) sk[i] = 0ull;
+    __syncthreads();
+    // bitonic sort, descending
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < P / 2; t += kSampThreads) {
+          const int i = 2 * t - (t & (stride - 1));
+          const int j = i + stride;
+          const bool desc = (i & size) == 0;
+          const uint64_t x = sk[i], y = sk[j];
+          if ((x < y) == desc) {
+            sk[i] = y;
+            sk[j] = x;
           }
-          __syncthreads();
         }
+        __syncthreads();
       }
     }
     // (4) probabilities p_i = exp(v_i - max); repack as (p bits << 32 | id)
