@@ -998,7 +998,10 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     // of this size delays the exchange that follows it: ahead of the q/k/v, x_mid or x_f
     // exchange by 2-3 us each, ahead of the attention all-gather (whose split counter and
     // combine are latency-bound) far less; all three here measured 557 us per step against
-    // 596 us with each issued after the phase before its own use.
+    // 596 us with each issued after the phase before its own use.  The barrier puts the
+    // publisher's exchange stores (the attention partial) ahead of the burst in the memory
+    // pipeline (547 against 557 us).
+    __syncthreads();
     if (loader) load_slots<BITS, PT>(wf, Ly.fc, m_fc, ll);
     if (loader) load_slots<BITS, PT>(wm, Ly.mproj, m_mp, ll);
     if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wq, a.layers[l + 1].attn, m_qkv, ll);
@@ -1058,7 +1061,8 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     __syncthreads();
     if (pub) publish_rows(a.x_x, d, B, b, out, m_mp.rows, ep + 6u, lane);
     // the next layer's c_proj slice (its registers are free once this layer's c_proj is
-    // done), issued once the phase's outputs are out
+    // done), issued after the phase's exchange stores (barrier: 535 against 547 us)
+    __syncthreads();
     if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wp, a.layers[l + 1].proj, m_proj, ll);
   }
   // ---------------- head: ln_f, final_norm, mel_head rows -> logits ------------------
