@@ -79,13 +79,10 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
 // 64 unnormalised outputs) to part [n_head][max_splits][66]; the consumer (the c_proj
 // GEMV's kProAttn prologue) combines them.
 int attn_decode_max_splits(int max_seq);
-// Batched decode attention (grid head x split x sequence) with the split combine into the
-// sequences' attention rows [B][d] in split form done by each (sequence, head)'s last split;
-// cnt holds B x n_head arrival counters, zero before the first launch (they wrap back to
-// zero); finished sequences are skipped.
-hipError_t launch_decode_batch_parts(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
-                                     int max_seq, float *part, uint32_t *cnt, const SplitOut &out, int kvt,
-                                     hipStream_t s);
+// Batched decode attention, one 16-wave block per (head, sequence), into the sequences'
+// attention rows [B][d] in split form; finished sequences are skipped.
+hipError_t launch_decode_batch_rows(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
+                                    int max_seq, const SplitOut &out, int kvt, hipStream_t s);
 // x[b] = mel_emb[tok_b] + mel_pos[pos_b] from the sequences' control blocks.
 hipError_t launch_embed_batch(const BatchSeq *seqs, int B, const float *mel_emb, const float *mel_pos, int d, float *x,
                               hipStream_t s);

@@ -457,71 +457,41 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
   attn_decode_block<KVT>(q, kc, vc, max_seq, ctl, static_len, part, blockIdx.x, blockIdx.y, gridDim.y, sh);
 }
 
-// Batched decode attention: grid (head, split, sequence); sequence b reads its query row
-// q[b], its cache (layer offset layer_off from its base) and its length from its control
-// block, and writes its partials at part + b * n_head * n_splits * 66 (write-through).  The
-// last split of a (sequence, head) to finish (wrapping device-scope counter cnt[b][h], zero
-// between launches) combines the partials in split order (global max, then the weighted
-// denominators and outputs) into the sequence's attention row in the GEMM's split form.
+// Batched decode attention, one block per (head, sequence): 16 waves, wave w over a
+// contiguous run of the sequence's 64-key tiles (attn_range), merged in LDS in wave order
+// into the sequence's attention row in the GEMM's split form; no partials leave the block.
 template <int KVT>
-__global__ __launch_bounds__(256) void attn_decode_batch_kernel(const float *q, const BatchSeq *seqs, size_t layer_off,
-                                                                int max_seq, float *part, uint32_t *cnt,
-                                                                SplitOut out) {
-  const BatchSeq &sq = seqs[blockIdx.z];
+__global__ __launch_bounds__(1024) void attn_decode_batch_row_kernel(const float *q, const BatchSeq *seqs,
+                                                                    size_t layer_off, int max_seq, SplitOut out) {
+  const BatchSeq sq = seqs[blockIdx.y];
   if (sq.ctl->done) return;
-  __shared__ AttnShared sh;
-  __shared__ uint32_t last;
-  const int H = gridDim.x, d = H * 64, h = blockIdx.x, s = blockIdx.y, b = blockIdx.z, NS = gridDim.y;
-  const int S = (sq.ctl->valid_len + 1 + kAttnKeys - 1) / kAttnKeys;  // active splits
-  if (s >= S) return;
-  const size_t es = KVT == kKvBf16 ? 2 : 4;
+  __shared__ float so[16][64], sm[16], sl[16];
+  const int H = gridDim.x, d = H * 64, h = blockIdx.x, b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int L = sq.ctl->valid_len + 1, per = ((L + 63) / 64 + 15) / 16;  // tiles per wave
+  const int j0 = min(wave * per * 64, L), j1 = min((wave + 1) * per * 64, L);
+  const size_t es = KVT == kKvBf16 ? 2 : 4, hb = (size_t)h * max_seq * 64;
   const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
   const void *vc = static_cast<const char *>(sq.v) + layer_off * es;
-  float *pb = part + (size_t)b * H * NS * 66;
-  attn_decode_block<KVT, true>(q + (size_t)b * d, kc, vc, max_seq, sq.ctl, 0, pb, h, s, NS, sh);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this block's partial is stored
+  float m, l, o;
+  attn_range<KVT>(q + (size_t)b * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), j0, j1, m, l, o);
+  so[wave][lane] = o;
+  if (lane == 0) {
+    sm[wave] = m;
+    sl[wave] = l;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) last = atomicInc(cnt + (size_t)b * H + h, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
-  __syncthreads();
-  if (!last || threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  const uint32_t *ph = reinterpret_cast<const uint32_t *>(pb + (size_t)h * NS * 66);
-  auto ld = [&](int i) {
-    return __uint_as_float(__hip_atomic_load(ph + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  };
-  // every split's (max, denominator, output) loaded before the first use when they fit
-  // kCombineRegs registers each (one round trip), else split by split; same order and
-  // arithmetic either way
-  constexpr int kCombineRegs = 16;
-  float M = -INFINITY, den = 0.0f, num = 0.0f;
-  if (S <= kCombineRegs) {
-    float mv[kCombineRegs], lv[kCombineRegs], ov[kCombineRegs];
+  if (wave != 0) return;
+  float M = -INFINITY;
 #pragma unroll
-    for (int s2 = 0; s2 < kCombineRegs; s2++)
-      if (s2 < S) {
-        mv[s2] = ld(s2 * 66);
-        lv[s2] = ld(s2 * 66 + 1);
-        ov[s2] = ld(s2 * 66 + 2 + lane);
-      }
+  for (int w = 0; w < 16; w++) M = fmaxf(M, sm[w]);
+  float den = 0.0f, num = 0.0f;
 #pragma unroll
-    for (int s2 = 0; s2 < kCombineRegs; s2++)
-      if (s2 < S) M = fmaxf(M, mv[s2]);
-#pragma unroll
-    for (int s2 = 0; s2 < kCombineRegs; s2++)
-      if (s2 < S && mv[s2] != -INFINITY) {
-        const float f = __expf(mv[s2] - M);
-        den += lv[s2] * f;
-        num += ov[s2] * f;
-      }
-  } else {
-    for (int s2 = 0; s2 < S; s2++) M = fmaxf(M, ld(s2 * 66));
-    for (int s2 = 0; s2 < S; s2++) {
-      const float m = ld(s2 * 66);
-      if (m == -INFINITY) continue;
-      const float f = __expf(m - M);
-      den += ld(s2 * 66 + 1) * f;
-      num += ld(s2 * 66 + 2 + lane) * f;
-    }
+  for (int w = 0; w < 16; w++) {
+    if (sm[w] == -INFINITY) continue;
+    const float f = __expf(sm[w] - M);
+    den += sl[w] * f;
+    num += so[w][lane] * f;
   }
   const float v = num / den;
   uint32_t hi, lo;
@@ -753,17 +723,13 @@ hipError_t launch_gemv(const GemvArgs &a, int bits, int ptype, int pro, int epi,
 
 int attn_decode_max_splits(int max_seq) { return (max_seq + kAttnKeys - 1) / kAttnKeys; }
 
-hipError_t launch_decode_batch_parts(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
-                                     int max_seq, float *part, uint32_t *cnt, const SplitOut &out, int kvt,
-                                     hipStream_t s) {
-  const int S = attn_decode_max_splits(max_seq);
-  dim3 grid(n_head, S, B);
+hipError_t launch_decode_batch_rows(const float *q, const BatchSeq *seqs, int B, size_t layer_off, int n_head,
+                                    int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
+  dim3 grid(n_head, B);
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvBf16>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part,
-                       cnt, out);
+    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvBf16>, grid, dim3(1024), 0, s, q, seqs, layer_off, max_seq, out);
   } else {
-    hipLaunchKernelGGL(attn_decode_batch_kernel<kKvF32>, grid, dim3(256), 0, s, q, seqs, layer_off, max_seq, part,
-                       cnt, out);
+    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvF32>, grid, dim3(1024), 0, s, q, seqs, layer_off, max_seq, out);
   }
   return hipGetLastError();
 }

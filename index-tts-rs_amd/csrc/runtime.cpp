@@ -164,7 +164,7 @@ struct itts_gpt {
   int n_align = 2;
   // batched decode: residual rows, q rows, split-form rows, attention partials, logits,
   // the per-sequence descriptors and sampling parameters
-  DevBuf bx, bq, bpart, bcnt, blog, bseqs, bps;
+  DevBuf bx, bq, blog, bseqs, bps;
   SplitBuf bh, ba, bf;
   // sampler API scratch
   DevBuf s_logits, s_seen, s_rng, s_tok;
@@ -678,17 +678,12 @@ itts_status prepare_batch(itts_gpt *g, itts_kv *const *caches, int B) {
       if (caches[j] == kv) return set_error(ITTS_E_VALIDATION, "kv_cache: a cache appears twice in the batch");
     seqs[b] = BatchSeq{kv->ctl.as<DecodeCtl>(), kv->k.p, kv->v.p, kv->codes.as<int32_t>()};
   }
-  const int d = c.d_model, ms = caches[0]->max_seq;
+  const int d = c.d_model;
   HIP_TRY(g->bx.ensure(sizeof(float) * (size_t)B * d));
   HIP_TRY(g->bq.ensure(sizeof(float) * (size_t)B * d));
   HIP_TRY(g->bh.ensure(B, d));
   HIP_TRY(g->ba.ensure(B, d));
   HIP_TRY(g->bf.ensure(B, c.d_ffn));
-  HIP_TRY(g->bpart.ensure(sizeof(float) * (size_t)B * c.n_head * attn_decode_max_splits(ms) * 66));
-  // attention split counters: zero before the batch's first step (each launch leaves them
-  // at zero); cleared here, outside any captured graph
-  HIP_TRY(g->bcnt.ensure(sizeof(uint32_t) * (size_t)B * c.n_head));
-  HIP_TRY(hipMemsetAsync(g->bcnt.p, 0, sizeof(uint32_t) * (size_t)B * c.n_head, g->stream));
   HIP_TRY(g->blog.ensure(sizeof(float) * (size_t)B * c.mel_vocab));
   HIP_TRY(g->bseqs.ensure(sizeof(BatchSeq) * B));
   HIP_TRY(hipMemcpyAsync(g->bseqs.p, seqs.data(), sizeof(BatchSeq) * B, hipMemcpyHostToDevice, g->stream));
@@ -722,8 +717,8 @@ itts_status enqueue_step_batch(itts_gpt *g, int B, int max_seq, int kvt) {
       HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, B, d, g->bh.out(), s));
     ga.qkv = QkvDst{g->bq.as<float>(), nullptr, nullptr, max_seq, 0, d, seqs, layer_elems * l};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kvt, s));
-    HIP_TRY(launch_decode_batch_parts(g->bq.as<float>(), seqs, B, layer_elems * l, c.n_head, max_seq,
-                                      g->bpart.as<float>(), g->bcnt.as<uint32_t>(), g->ba.out(), kvt, s));
+    HIP_TRY(launch_decode_batch_rows(g->bq.as<float>(), seqs, B, layer_elems * l, c.n_head, max_seq, g->ba.out(),
+                                     kvt, s));
     ga = gemm_args(g, L.proj, g->ba.act(), B);
     ga.y = X;
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kvt, s));
