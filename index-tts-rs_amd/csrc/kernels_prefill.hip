@@ -516,13 +516,17 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
 // ---- few-row products (M <= 8: the batched decode step) ---------------------------------
 // The 64-row tiles above spend most of a launch filling the ring for a few real rows.  Here
 // a block of kFewWaves waves takes 64 output columns (two 32-column MFMA tiles) over
-// kFewWaves gw K groups, gw per wave (issued together), with no LDS staging: each lane loads its activation and code
+// kFewWaves K groups, one per wave, with no LDS staging: each lane loads its activation and code
 // fragments straight into registers (a lane's 16 codes of a column are one 16-byte load,
 // its 16 activations of a row two), in the K order the tiles above use.  Rows past M are
 // zero fragments; in the 32 x 32 result a lane's rows 4h .. 4h+3 (h = lane >> 5) are the
 // only live ones.  The waves' partials are added in wave order in LDS; the K splits
 // (blocks) in split order by the last block of the column tile to arrive, as above.
-constexpr int kFewRows = 8, kFewMaxGw = 2, kFewMaxSplits = 16;
+// One K group per wave (K <= 8192; longer K takes the tiled GEMM): the register arrays
+// sized for one group keep the kernel at 92-98 VGPRs (128-132 with the folded LayerNorm),
+// so two blocks share a compute unit and mel_head's 387 blocks run in one round (batched
+// decode 5,915 -> 6,134 tok/s against arrays sized for two groups).
+constexpr int kFewRows = 8, kFewMaxGw = 1, kFewMaxSplits = 16;
 // eight waves per block measured 3 % faster on batched decode than four (half the K
 // splits) and 23 % faster than two
 constexpr int kFewWaves = 8;                  // waves per block, a K group each
@@ -1059,7 +1063,8 @@ hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt,
       return hipErrorInvalidValue;
   }
   if (a.M <= kFewRows && (bits == 8 || bits == 4)) {
-    // a group per wave while that keeps the splits within kFewMaxSplits, else two
+    // a group per wave while that keeps the splits within kFewMaxSplits (gw > kFewMaxGw
+    // beyond that: the tiled GEMM)
     const int nN = (a.ql.N + 63) / 64, G = a.ql.K / kGroup;
     const int gw = (G + kFewWaves * kFewMaxSplits - 1) / (kFewWaves * kFewMaxSplits);
     const int S = (G + kFewWaves * gw - 1) / (kFewWaves * gw);
