@@ -457,18 +457,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
   attn_decode_block<KVT>(q, kc, vc, max_seq, ctl, static_len, part, blockIdx.x, blockIdx.y, gridDim.y, sh);
 }
 
-// Batched decode attention, one block per (head, sequence): 16 waves, wave w over a
+// Batched decode attention, one block per (head, sequence): RW waves (16 for bf16 rows; 8
+// for fp32 rows, whose tile registers would not fit 16 waves' 128 VGPRs), wave w over a
 // contiguous run of the sequence's 64-key tiles (attn_range), merged in LDS in wave order
 // into the sequence's attention row in the GEMM's split form; no partials leave the block.
 template <int KVT>
-__global__ __launch_bounds__(1024) void attn_decode_batch_row_kernel(const float *q, const BatchSeq *seqs,
-                                                                    size_t layer_off, int max_seq, SplitOut out) {
+constexpr int row_waves() {
+  return KVT == kKvBf16 ? 16 : 8;
+}
+template <int KVT>
+__global__ __launch_bounds__(64 * row_waves<KVT>()) void attn_decode_batch_row_kernel(const float *q,
+                                                                                     const BatchSeq *seqs,
+                                                                                     size_t layer_off, int max_seq,
+                                                                                     SplitOut out) {
+  constexpr int RW = row_waves<KVT>();
   const BatchSeq sq = seqs[blockIdx.y];
   if (sq.ctl->done) return;
-  __shared__ float so[16][64], sm[16], sl[16];
+  __shared__ float so[RW][64], sm[RW], sl[RW];
   const int H = gridDim.x, d = H * 64, h = blockIdx.x, b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int L = sq.ctl->valid_len + 1, per = ((L + 63) / 64 + 15) / 16;  // tiles per wave
+  const int L = sq.ctl->valid_len + 1, per = ((L + 63) / 64 + RW - 1) / RW;  // tiles per wave
   const int j0 = min(wave * per * 64, L), j1 = min((wave + 1) * per * 64, L);
   const size_t es = KVT == kKvBf16 ? 2 : 4, hb = (size_t)h * max_seq * 64;
   const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
@@ -484,10 +492,10 @@ __global__ __launch_bounds__(1024) void attn_decode_batch_row_kernel(const float
   if (wave != 0) return;
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < 16; w++) M = fmaxf(M, sm[w]);
+  for (int w = 0; w < RW; w++) M = fmaxf(M, sm[w]);
   float den = 0.0f, num = 0.0f;
 #pragma unroll
-  for (int w = 0; w < 16; w++) {
+  for (int w = 0; w < RW; w++) {
     if (sm[w] == -INFINITY) continue;
     const float f = __expf(sm[w] - M);
     den += sl[w] * f;
@@ -727,9 +735,11 @@ hipError_t launch_decode_batch_rows(const float *q, const BatchSeq *seqs, int B,
                                     int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
   dim3 grid(n_head, B);
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvBf16>, grid, dim3(1024), 0, s, q, seqs, layer_off, max_seq, out);
+    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvBf16>, grid, dim3(64 * row_waves<kKvBf16>()), 0, s, q, seqs,
+                       layer_off, max_seq, out);
   } else {
-    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvF32>, grid, dim3(1024), 0, s, q, seqs, layer_off, max_seq, out);
+    hipLaunchKernelGGL(attn_decode_batch_row_kernel<kKvF32>, grid, dim3(64 * row_waves<kKvF32>()), 0, s, q, seqs,
+                       layer_off, max_seq, out);
   }
   return hipGetLastError();
 }
