@@ -146,10 +146,29 @@ struct FoldIn {
   const float *x, *gamma, *G, *c;
 };
 
+// The same fold in the tiled product (any M): the input planes already hold gamma * x
+// (written by the residual product before it, TileFoldOut), st[m][K/64] holds the mean
+// and the sum of squared deviations of each 64-column group of row m of x, and the
+// epilogue applies rstd (sum - mean G[n]) + c[n] with the row's statistics combined from
+// its groups (equal-size groups: mean of the means, M2 = sum M2_g + 64 sum (mean_g - mean)^2).
+struct TileFoldIn {
+  const float2 *st;
+  const float *G, *c;
+};
+// Residual epilogue that also writes the next folded LayerNorm's input from the updated
+// rows x: gamma * x in split form (planes and group sums) and the group statistics of x.
+struct TileFoldOut {
+  SplitOut o;
+  const float *gamma;
+  float2 *st;       // [M][N/64]
+};
+
 struct GemmArgs {
   DevQL ql;
   SplitAct x;       // [M][K] (unused with fold.x)
   FoldIn fold;      // fold.x set: the input is LayerNorm(x) by the fold above
+  TileFoldIn tfi;   // tfi.st set (tiled product, QKV or GELU epilogue): folded LayerNorm input
+  TileFoldOut tfo;  // tfo.st set (tiled product, residual epilogue): write the next fold's input
   int M;
   float *y;         // [M][N] (store) or residual stream [M][N] (resid)
   SplitOut xo;      // gelu: the next GEMM's input [M][N] (N a multiple of 64)
@@ -163,6 +182,8 @@ struct GemmArgs {
   int n_cu;         // compute units (grid sizing)
 };
 hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt, hipStream_t s);
+// The tiled product uses 64 x 64 tiles up to this many rows, 128 x 128 tiles above.
+constexpr int kGemmSmallTileRows = 512;
 // Sets the LDS attributes of every GEMM instantiation (before any graph capture).
 hipError_t gemm_init();
 size_t gemm_ws_floats(int n_cu);

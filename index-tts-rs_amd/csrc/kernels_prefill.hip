@@ -57,6 +57,17 @@ struct Shape {
 __device__ __forceinline__ int swz_act(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int swz_codes(int bits, int r) { return bits == 8 ? (r >> 2) & 3 : (r >> 3) & 1; }
 
+// Sum over the TPI consecutive lanes of an item: nothing (1) or a DPP quad (4).
+template <int TPI>
+__device__ __forceinline__ float item_sum(float v) {
+  static_assert(TPI == 1 || TPI == 4, "item width");
+  if constexpr (TPI == 4) {
+    v += dpp_pair<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_pair<0x4E>(v);  // quad_perm [2,3,0,1]
+  }
+  return v;
+}
+
 // two consecutive 8-bit codes (bits sh..sh+15 of w) -> packed fp16 pair (exact)
 __device__ __forceinline__ uint32_t f16_pair_u8(uint32_t w, int sh) {
   const float lo = (float)((w >> sh) & 0xffu);
@@ -335,6 +346,47 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
 
   if (copier)
     for (int i = 0; i < NS - 1 && i < ng; i++) issue(g0 + i, stage(i));
+  // Folded LayerNorm input: each row's mean and rstd from its groups' statistics.  A quad of
+  // worker lanes a row (64 rows per pass of the four worker waves), lane p of the quad
+  // holding groups p, p + 4, ... (K <= 2048: at most 8), the quad's sums formed by two DPP
+  // quad permutes.  On 64-row tiles the loads are issued here, before the K loop (nothing
+  // else of the workers' waits on the vector-memory counter), and reduced after it; 128-row
+  // tiles (no registers to spare) load after the loop.
+  constexpr bool kFoldIn = EPI == kEpiQKV || EPI == kEpiGelu;
+  constexpr int kFoldGpl = 8;  // groups a lane
+  constexpr bool kFoldEarly = kFoldIn && TM == 1;
+  __shared__ float2 fold_row[kFoldIn ? BM : 1];
+  const bool fin = kFoldIn && a.tfi.st != nullptr;
+  float2 fv[kFoldEarly ? kFoldGpl : 1];
+  auto fold_load = [&](int pass, float2 *v) __attribute__((always_inline)) {
+    const int m = min(m0 + pass * 64 + ((tid & 255) >> 2), M - 1), p = tid & 3;
+#pragma unroll
+    for (int i = 0; i < kFoldGpl; i++) {
+      const int g = p + 4 * i;
+      v[i] = g < G ? a.tfi.st[(size_t)m * G + g] : make_float2(0.0f, 0.0f);
+    }
+  };
+  auto fold_reduce = [&](int pass, const float2 *v) __attribute__((always_inline)) {
+    const int p = tid & 3;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kFoldGpl; i++) sum += v[i].x;
+    sum += dpp_pair<0xB1>(sum);  // quad_perm [1,0,3,2]
+    sum += dpp_pair<0x4E>(sum);  // quad_perm [2,3,0,1]
+    const float mean = sum / (float)G;
+    float m2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kFoldGpl; i++) {
+      const float dm = v[i].x - mean;
+      if (p + 4 * i < G) m2 += v[i].y + 64.0f * (dm * dm);
+    }
+    m2 += dpp_pair<0xB1>(m2);
+    m2 += dpp_pair<0x4E>(m2);
+    if (p == 0) fold_row[pass * 64 + ((tid & 255) >> 2)] = make_float2(mean, 1.0f / sqrtf(m2 / (float)K + 1e-5f));
+  };
+  if constexpr (kFoldEarly) {
+    if (fin && worker) fold_load(0, fv);
+  }
   int i = 0;
   for (; i + 1 < ng; i += 2) {
     step(i, P0, P1);
@@ -345,6 +397,22 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     if (worker && !PROD) apply(P0);
   } else {
     if (worker && !PROD) apply(P1);
+  }
+
+  if constexpr (kFoldIn) {
+    if (fin && worker) {
+      if constexpr (kFoldEarly) {
+        fold_reduce(0, fv);
+      } else {
+#pragma unroll
+        for (int pass = 0; pass < TM; pass++) {
+          float2 v[kFoldGpl];
+          fold_load(pass, v);
+          fold_reduce(pass, v);
+        }
+      }
+    }
+    if (fin) __syncthreads();  // rows reduced by one wave are read by the others
   }
 
   const int tile = t.tm * nN + t.tn;
@@ -414,6 +482,96 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     }
   }
 
+  if constexpr (EPI == kEpiResid) {
+    if (a.tfo.st) {
+      // The updated rows x staged in LDS, then per (row, 64-column group): the group's mean
+      // and sum of squared deviations of x, and gamma * x as the next GEMM's input (hi/lo
+      // planes and the group sum).
+      constexpr int LDT = BN + 1;
+      constexpr int GPR = BN / 64, ITEMS = BM * GPR, TPI = 256 / ITEMS, VPT = 64 / TPI;
+      static_assert(ITEMS * TPI == 256 && VPT % 8 == 0, "fold epilogue shape");
+      float *T = reinterpret_cast<float *>(lds);
+      // this thread's item (row rl, 64-column group grp, values c0 .. c0 + VPT - 1); its
+      // gamma values are loaded first, under the staging below (16-byte aligned: the
+      // vector starts on 256 bytes and c0 is a multiple of 16)
+      const int item = tid / TPI, sub = tid % TPI;
+      const int rl = item / GPR, grp = item % GPR;
+      const int c0 = grp * 64 + sub * VPT;
+      // N is a multiple of 64: a group is wholly in or out
+      const bool live = worker && m0 + rl < M && n0 + c0 < N;
+      float4 gam[VPT / 4];
+#pragma unroll
+      for (int c = 0; c < VPT / 4; c++)
+        gam[c] = live ? reinterpret_cast<const float4 *>(a.tfo.gamma + n0 + c0)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      __syncthreads();
+      if (worker)
+#pragma unroll
+        for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            const int cl = wn * 32 * TN + j * 32 + (lane & 31), n = n0 + cl;
+            if (n >= N) continue;
+            const float bias = a.ql.bias[n];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+              const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+              const int m = m0 + rl;
+              if (m >= M) continue;
+              const float v = a.y[(size_t)m * N + n] + (acc[i2][j][e] + bias);
+              a.y[(size_t)m * N + n] = v;
+              T[rl * LDT + cl] = v;
+            }
+          }
+      __syncthreads();
+      if (worker) {
+        const int m = m0 + rl, n = n0 + c0;
+        float xv[VPT];
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < VPT; c++) {
+          xv[c] = T[rl * LDT + c0 + c];
+          sum += xv[c];
+        }
+        sum = item_sum<TPI>(sum);
+        const float mean = sum / 64.0f;
+        float m2 = 0.0f, gsum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < VPT; c += 8) {
+          uint32_t hw[4], lw[4];
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float v0 = xv[c + e], v1 = xv[c + e + 1];
+            const float d0 = v0 - mean, d1 = v1 - mean;
+            m2 += d0 * d0;
+            m2 += d1 * d1;
+            const float4 gq = gam[(c + e) >> 2];
+            const float g0 = ((e & 2) ? gq.z : gq.x) * v0;
+            const float g1 = ((e & 2) ? gq.w : gq.y) * v1;
+            gsum += g0;
+            gsum += g1;
+            uint32_t h0, l0, h1, l1;
+            split_f16(g0, h0, l0);
+            split_f16(g1, h1, l1);
+            hw[e >> 1] = h0 | (h1 << 16);
+            lw[e >> 1] = l0 | (l1 << 16);
+          }
+          if (live) {
+            *reinterpret_cast<uint4 *>(a.tfo.o.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            *reinterpret_cast<uint4 *>(a.tfo.o.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+          }
+        }
+        m2 = item_sum<TPI>(m2);
+        gsum = item_sum<TPI>(gsum);
+        if (live && sub == 0) {
+          const size_t gi = (size_t)m * (N / kGroup) + (n0 + grp * 64) / kGroup;
+          a.tfo.o.gs[gi] = gsum;
+          a.tfo.st[gi] = make_float2(mean, m2);
+        }
+      }
+      return;
+    }
+  }
+
   if constexpr (EPI == kEpiGelu) {
     // GELU tile staged in LDS, then written as the next GEMM's input: hi/lo planes and
     // the per-64-column row sums
@@ -426,11 +584,15 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const int cl = wn * 32 * TN + j * 32 + (lane & 31);
-        const float bias = n0 + cl < N ? a.ql.bias[n0 + cl] : 0.0f;
+        const bool nl = n0 + cl < N;
+        const float bias = nl ? (fin ? a.tfi.c[n0 + cl] : a.ql.bias[n0 + cl]) : 0.0f;
+        const float gn = fin && nl ? a.tfi.G[n0 + cl] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          T[rl * LDT + cl] = gelu_tanh(acc[i2][j][e] + bias);
+          float v = acc[i2][j][e];
+          if (fin) v = fold_row[rl].y * (v - fold_row[rl].x * gn);
+          T[rl * LDT + cl] = gelu_tanh(v + bias);
         }
       }
     __syncthreads();
@@ -462,8 +624,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
           *reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         }
       }
-#pragma unroll
-      for (int o = 1; o < TPI; o <<= 1) sum += __shfl_xor(sum, o, 64);
+      sum = item_sum<TPI>(sum);
       if (live && sub == 0) a.xo.gs[(size_t)m * (N / kGroup) + n / kGroup] = sum;
     }
     return;
@@ -474,12 +635,16 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       for (int j = 0; j < TN; j++) {
         const int n = n0 + wn * 32 * TN + j * 32 + (lane & 31);
         if (n >= N) continue;
-        const float bias = a.ql.bias[n];
+        const float bias = fin ? a.tfi.c[n] : a.ql.bias[n];
+        const float gn = fin ? a.tfi.G[n] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const int m = m0 + wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          const int m = m0 + rl;
           if (m >= M) continue;
-          const float v = acc[i2][j][e] + bias;
+          float v = acc[i2][j][e];
+          if (fin) v = fold_row[rl].y * (v - fold_row[rl].x * gn);
+          v += bias;
           if constexpr (EPI == kEpiStore) {
             a.y[(size_t)m * N + n] = v;
           } else if constexpr (EPI == kEpiResid) {
@@ -910,7 +1075,7 @@ constexpr size_t lds_bytes() {
 
 Plan make_plan(const GemmArgs &a, int bits, int ptype) {
   Plan p{};
-  const bool large = a.M > 512;
+  const bool large = a.M > kGemmSmallTileRows;
   p.TM = p.TN = large ? 2 : 1;
   const int BM = 64 * p.TM, BN = 64 * p.TN;
   const int G = a.ql.K / kGroup;
@@ -1062,7 +1227,13 @@ hipError_t launch_gemm(const GemmArgs &a, int bits, int ptype, int epi, int kvt,
         (epi != kEpiQKV && epi != kEpiGelu) || !a.fold.gamma || !a.fold.G || !a.fold.c)
       return hipErrorInvalidValue;
   }
-  if (a.M <= kFewRows && (bits == 8 || bits == 4)) {
+  if (a.tfi.st && ((epi != kEpiQKV && epi != kEpiGelu) || a.ql.K > 32 * kGroup || !a.tfi.G || !a.tfi.c || a.fold.x))
+    return hipErrorInvalidValue;
+  if (a.tfo.st && (epi != kEpiResid || a.ql.N % kGroup != 0 || !a.tfo.gamma || !a.tfo.o.hi || !a.tfo.o.lo ||
+                   !a.tfo.o.gs || a.fold.x))
+    return hipErrorInvalidValue;
+  // (the tiled folds are written for the tiled product only)
+  if (a.M <= kFewRows && (bits == 8 || bits == 4) && !a.tfi.st && !a.tfo.st) {
     // a group per wave while that keeps the splits within kFewMaxSplits (gw > kFewMaxGw
     // beyond that: the tiled GEMM)
     const int nN = (a.ql.N + 63) / 64, G = a.ql.K / kGroup;

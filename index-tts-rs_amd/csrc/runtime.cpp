@@ -156,6 +156,8 @@ struct itts_gpt {
   // split form (LN output, attention output, GELU output), split-K partials and counters
   DevBuf px, pq, rows, conds;
   SplitBuf ph, pa, pf;
+  // the folded LayerNorms' group statistics of the residual rows [M][d/64] (mean, M2)
+  DevBuf pst;
   DevBuf gws, gcnt;
   // replay / all-row forward: per-layer scratch K/V (fp32 [n_head][M][64]), key starts,
   // head logits, probe maps, codes and log-probabilities
@@ -293,8 +295,35 @@ itts_status ensure_rows(itts_gpt *g, int M) {
   HIP_TRY(g->pq.ensure(sizeof(float) * (size_t)M * d));
   HIP_TRY(g->pa.ensure(M, d));
   HIP_TRY(g->pf.ensure(M, g->cfg.d_ffn));
+  HIP_TRY(g->pst.ensure(sizeof(float2) * (size_t)M * (d / kGroup)));
   return ITTS_OK;
 }
+
+// LayerNorms of the multi-row stacks after layer 0's ln_1 folded into the products: each
+// residual product writes gamma * x of the next LayerNorm in split form with the group
+// statistics of x (TileFoldOut), and the QKV / c_fc product applies them (TileFoldIn).
+// Layer 0's ln_1 input comes from the embeddings and keeps its row kernel.  Used on the
+// 64 x 64 tiles (235-row prefill 2.42 -> 2.35 ms on MI355X); on 128 x 128 tiles the fold's
+// epilogues cost more than the row kernels (4 x 547 rows: 11.05 -> 11.32 ms), and d <= 2048
+// (the statistics' reduction holds at most 32 groups a row).
+struct StackFold {
+  bool on;
+  size_t per;
+  const float *fold;
+  float2 *st;
+  int d, F;
+  StackFold(const itts_gpt *g, int M) {
+    d = g->cfg.d_model;
+    F = g->cfg.d_ffn;
+    on = g->fold.p != nullptr && d % kGroup == 0 && d <= 32 * kGroup && M <= kGemmSmallTileRows;
+    per = fold_floats(d, F);
+    fold = g->fold.as<float>();
+    st = g->pst.as<float2>();
+  }
+  TileFoldIn qkv(int l) const { return TileFoldIn{st, fold + per * l, fold + per * l + 3 * d}; }
+  TileFoldIn fc(int l) const { return TileFoldIn{st, fold + per * l + 6 * d, fold + per * l + 6 * d + F}; }
+  TileFoldOut out(const SplitBuf &b, const float *gamma) const { return TileFoldOut{b.out(), gamma, st}; }
+};
 
 itts_status validate_prefix(const itts_config &c, const int32_t *text, int32_t n_text,
                             const float *conds, int32_t n_cond, int32_t max_cond, int32_t lang,
@@ -363,10 +392,12 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
   hipStream_t s = g->stream;
   float *X = g->px.as<float>(), *Q = g->pq.as<float>();
   auto gemm = [&](const DevQL &ql, SplitAct x) { return gemm_args(g, ql, x, T); };
+  const StackFold sf(g, T);
   for (int l = 0; l < c.n_layer; l++) {
     const DevLayer &L = g->layers[l];
-    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, g->ph.out(), s));
+    if (!sf.on || l == 0) HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, T, d, g->ph.out(), s));
     GemmArgs ga = gemm(L.attn, g->ph.act());
+    if (sf.on && l > 0) ga.tfi = sf.qkv(l);
     ga.qkv = QkvDst{Q, kv->k_layer(l), kv->v_layer(l), kv->max_seq, 0, d};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kv->kvt, s));
     if (T <= kFlashMinRows) {  // few query tiles: one block per (head, row) spreads wider
@@ -378,13 +409,16 @@ itts_status enqueue_prefill_stack(itts_gpt *g, itts_kv *kv, int T) {
     }
     ga = gemm(L.proj, g->pa.act());
     ga.y = X;
+    if (sf.on) ga.tfo = sf.out(g->ph, L.ln2_w);
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
-    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, T, d, g->ph.out(), s));
+    if (!sf.on) HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, T, d, g->ph.out(), s));
     ga = gemm(L.fc, g->ph.act());
+    if (sf.on) ga.tfi = sf.fc(l);
     ga.xo = g->pf.out();
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kv->kvt, s));
     ga = gemm(L.mproj, g->pf.act());
     ga.y = X;
+    if (sf.on && l + 1 < c.n_layer) ga.tfo = sf.out(g->ph, g->layers[l + 1].ln1_w);
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kv->kvt, s));
   }
   GemvArgs ha{};
@@ -573,10 +607,12 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
   HIP_TRY(g->kstart.ensure(sizeof(int) * ks_order.size()));
   HIP_TRY(hipMemcpyAsync(g->kstart.p, ks_order.data(), sizeof(int) * ks_order.size(), hipMemcpyHostToDevice, s));
   float *X = g->px.as<float>(), *Q = g->pq.as<float>();
+  const StackFold sf(g, M);
   for (int l = 0; l < n_layers; l++) {
     const DevLayer &L = g->layers[l];
-    HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, M, d, g->ph.out(), s));
+    if (!sf.on || l == 0) HIP_TRY(launch_ln_rows(X, L.ln1_w, L.ln1_b, M, d, g->ph.out(), s));
     GemmArgs ga = gemm_args(g, L.attn, g->ph.act(), M);
+    if (sf.on && l > 0) ga.tfi = sf.qkv(l);
     ga.qkv = QkvDst{Q, g->rk.p, g->rv.p, M, 0, d};
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiQKV, kKvF32, s));
     for (const ProbeSpec &p : probes)  // read-only exports of this layer's attention
@@ -587,13 +623,16 @@ itts_status forward_rows_stack(itts_gpt *g, int M, const std::vector<int> &kstar
                               g->pkvs.as<uint16_t>(), g->kstart.as<int>() + M));
     ga = gemm_args(g, L.proj, g->pa.act(), M);
     ga.y = X;
+    if (sf.on) ga.tfo = sf.out(g->ph, L.ln2_w);
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
-    HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, M, d, g->ph.out(), s));
+    if (!sf.on) HIP_TRY(launch_ln_rows(X, L.ln2_w, L.ln2_b, M, d, g->ph.out(), s));
     ga = gemm_args(g, L.fc, g->ph.act(), M);
+    if (sf.on) ga.tfi = sf.fc(l);
     ga.xo = g->pf.out();
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiGelu, kKvF32, s));
     ga = gemm_args(g, L.mproj, g->pf.act(), M);
     ga.y = X;
+    if (sf.on && l + 1 < n_layers) ga.tfo = sf.out(g->ph, g->layers[l + 1].ln1_w);
     HIP_TRY(launch_gemm(ga, bits, pt, kEpiResid, kKvF32, s));
   }
   return ITTS_OK;

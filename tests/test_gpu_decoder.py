@@ -71,6 +71,24 @@ def test_prefill_and_steps_match_oracle(model, kvt):
     assert kv.valid_len() == okv.valid_len()
 
 
+@pytest.mark.parametrize("n_cond,n_text", [(0, 1), (1, 4), (30, 32), (64, 62)])
+def test_prefill_row_counts_match_oracle(model, n_cond, n_text):
+    """Prefills of 4, 8, 65 and 129 rows: products with at most 8 rows, which take the
+    tiled GEMM while their LayerNorms are folded, and ragged last 64-row tiles, where
+    the folded statistics of rows past the prompt must not leak into live rows."""
+    W, g, M = model
+    say(f"[gpu] prefill rows={n_cond + n_text + 3}")
+    pr = synth.make_prompt(W.cfg, n_cond, n_text, seed=n_cond + n_text)
+    kv, okv = g.kv_cache(256, H.ITTS_F32), M.kv(256, kv_bf16=False)
+    a = g.prefill(pr.text_tokens, pr.conds, pr.lang_id, kv)
+    b = M.prefill_after(okv, pr.text_tokens, pr.conds, pr.lang_id)
+    assert kv.valid_len() == okv.valid_len() == n_cond + n_text + 3
+    assert np.abs(a - b).max() < TIGHT_TOL
+    for l in range(W.cfg["n_layer"]):
+        for which in (0, 1):
+            assert np.allclose(kv.read(l, which), okv.read(l, which), rtol=1e-3, atol=1e-5)
+
+
 def test_prefill_after_equals_prefill_then_steps(model):
     W, g, _ = model
     say("[gpu] prefill_after self-consistency")
