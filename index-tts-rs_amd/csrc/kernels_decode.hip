@@ -457,39 +457,25 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *q, const 
   attn_decode_block<KVT>(q, kc, vc, max_seq, ctl, static_len, part, blockIdx.x, blockIdx.y, gridDim.y, sh);
 }
 
-// Batched decode attention, one block per (head, sequence): RW waves (16 for bf16 rows; 8
-// for fp32 rows, whose tile registers would not fit 16 waves' 128 VGPRs), wave w over a
-// contiguous run of the sequence's 64-key tiles (attn_range), merged in LDS in wave order
-// into the sequence's attention row in the GEMM's split form; no partials leave the block.
-template <int KVT>
-constexpr int row_waves() {
-  return KVT == kKvBf16 ? 16 : 8;
-}
-template <int KVT>
-__global__ __launch_bounds__(64 * row_waves<KVT>()) void attn_decode_batch_row_kernel(const float *q,
-                                                                                     const BatchSeq *seqs,
-                                                                                     size_t layer_off, int max_seq,
-                                                                                     SplitOut out) {
-  constexpr int RW = row_waves<KVT>();
-  const BatchSeq sq = seqs[blockIdx.y];
-  if (sq.ctl->done) return;
+// One query row attended by the RW waves of a block over keys [0, L): wave w takes a
+// contiguous run of the row's 64-key tiles (attn_range) and the runs are merged in LDS in
+// wave order; no partials leave the block.  True in wave 0, whose lane holds dimension
+// `lane` of the row's output in v; the other waves return false and leave.
+template <int KVT, int RW>
+__device__ __forceinline__ bool attn_row_merged(const float *q, const void *kh, const void *vh, int L, float &v) {
   __shared__ float so[RW][64], sm[RW], sl[RW];
-  const int H = gridDim.x, d = H * 64, h = blockIdx.x, b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int L = sq.ctl->valid_len + 1, per = ((L + 63) / 64 + RW - 1) / RW;  // tiles per wave
+  const int per = ((L + 63) / 64 + RW - 1) / RW;  // tiles per wave
   const int j0 = min(wave * per * 64, L), j1 = min((wave + 1) * per * 64, L);
-  const size_t es = KVT == kKvBf16 ? 2 : 4, hb = (size_t)h * max_seq * 64;
-  const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
-  const void *vc = static_cast<const char *>(sq.v) + layer_off * es;
   float m, l, o;
-  attn_range<KVT>(q + (size_t)b * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), j0, j1, m, l, o);
+  attn_range<KVT>(q, kh, vh, j0, j1, m, l, o);
   so[wave][lane] = o;
   if (lane == 0) {
     sm[wave] = m;
     sl[wave] = l;
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) return false;
   float M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < RW; w++) M = fmaxf(M, sm[w]);
@@ -501,7 +487,32 @@ __global__ __launch_bounds__(64 * row_waves<KVT>()) void attn_decode_batch_row_k
     den += sl[w] * f;
     num += so[w][lane] * f;
   }
-  const float v = num / den;
+  v = num / den;
+  return true;
+}
+
+// Batched decode attention, one block per (head, sequence): RW waves (16 for bf16 rows; 8
+// for fp32 rows, whose tile registers would not fit 16 waves' 128 VGPRs) over the
+// sequence's keys (attn_row_merged), into its attention row in the GEMM's split form.
+template <int KVT>
+constexpr int row_waves() {
+  return KVT == kKvBf16 ? 16 : 8;
+}
+template <int KVT>
+__global__ __launch_bounds__(64 * row_waves<KVT>()) void attn_decode_batch_row_kernel(const float *q,
+                                                                                     const BatchSeq *seqs,
+                                                                                     size_t layer_off, int max_seq,
+                                                                                     SplitOut out) {
+  const BatchSeq sq = seqs[blockIdx.y];
+  if (sq.ctl->done) return;
+  const int H = gridDim.x, d = H * 64, h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63;
+  const size_t es = KVT == kKvBf16 ? 2 : 4, hb = (size_t)h * max_seq * 64;
+  const void *kc = static_cast<const char *>(sq.k) + layer_off * es;
+  const void *vc = static_cast<const char *>(sq.v) + layer_off * es;
+  float v;
+  if (!attn_row_merged<KVT, row_waves<KVT>()>(q + (size_t)b * d + h * 64, head_base<KVT>(kc, hb),
+                                              head_base<KVT>(vc, hb), sq.ctl->valid_len + 1, v))
+    return;
   uint32_t hi, lo;
   split_f16(v, hi, lo);
   const size_t i = (size_t)b * d + h * 64 + lane;
@@ -537,6 +548,9 @@ __device__ inline void put_split(const SplitOut &o, size_t i, size_t gi, float v
   if ((threadIdx.x & 63) == 0) o.gs[gi] = s;
 }
 
+// Prefill attention, one wave per (head, row) over the row's keys in series.  (Four waves
+// a row, its tiles side by side and merged in LDS (attn_row_merged), made the 235-row
+// prefill 2.36 -> 2.44 ms: the short rows' idle waves cost more than the long rows gain.)
 template <int KVT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
                                                           const void *vc, int max_seq, int d,
