@@ -182,7 +182,8 @@ struct itts_kv {
   DevBuf ctl;          // DecodeCtl
   DevBuf part;         // attention split partials [n_head][splits][66]
   DevBuf codes;        // generate output
-  DecodeCtl *host_ctl = nullptr;  // pinned staging, 2 slots
+  DecodeCtl *host_ctl = nullptr;  // pinned staging, 2 slots, then the error word's copy
+  uint32_t *host_err() const { return reinterpret_cast<uint32_t *>(host_ctl + 2); }
   int splits = 0;
   // persistent decode step: exchange words, split counters + error word, arguments
   bool persist = false;
@@ -793,13 +794,15 @@ itts_status write_ctl(itts_kv *kv, const DecodeCtl &h) {
 // After the stream has drained: a persistent step whose exchange wait timed out leaves
 // the error word set and its step unfinished.  The exchange state is cleared so that the
 // cache stays usable, and the call reports a device error.
-itts_status check_persist(itts_kv *kv) {
-  if (!kv->persist) return ITTS_OK;
+// The persistent step's error word: its copy to pinned memory enqueued, then read after the
+// caller's next synchronisation (persist_err_check).
+hipError_t persist_err_enqueue(itts_kv *kv) {
+  if (!kv->persist) return hipSuccess;
+  return hipMemcpyAsync(kv->host_err(), kv->pa.err, sizeof(uint32_t), hipMemcpyDeviceToHost, kv->gpt->stream);
+}
+itts_status persist_err_check(itts_kv *kv) {
+  if (!kv->persist || *kv->host_err() == 0) return ITTS_OK;
   hipStream_t s = kv->gpt->stream;
-  uint32_t err = 0;
-  HIP_TRY(hipMemcpyAsync(&err, kv->pa.err, sizeof err, hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipStreamSynchronize(s));
-  if (err == 0) return ITTS_OK;
   HIP_TRY(hipMemsetAsync(kv->xch.p, 0, kv->xch.bytes, s));
   HIP_TRY(hipMemsetAsync(kv->sync.p, 0, kv->sync.bytes, s));
   // epochs restart with the cleared words (an exchange word keeps 16 epoch bits, so a
@@ -807,6 +810,11 @@ itts_status check_persist(itts_kv *kv) {
   HIP_TRY(hipMemsetAsync(static_cast<char *>(kv->ctl.p) + offsetof(DecodeCtl, xstep), 0, sizeof(int32_t), s));
   HIP_TRY(hipStreamSynchronize(s));
   return set_error(ITTS_E_DEVICE, "decode step: a persistent-kernel exchange wait timed out");
+}
+itts_status check_persist(itts_kv *kv) {
+  HIP_TRY(persist_err_enqueue(kv));
+  HIP_TRY(hipStreamSynchronize(kv->gpt->stream));
+  return persist_err_check(kv);
 }
 
 // Sets up the persistent decode step for a new cache when the decoder and the cache
@@ -1109,7 +1117,7 @@ itts_status itts_kv_create(itts_gpt *gpt, int32_t max_seq, itts_dtype kv_dtype, 
   if (kv->k.ensure(n * es) || kv->v.ensure(n * es) || kv->ctl.ensure(sizeof(DecodeCtl)) ||
       kv->part.ensure(sizeof(float) * (size_t)gpt->cfg.n_head * kv->splits * 66) ||
       kv->codes.ensure(sizeof(int32_t) * 2048) ||
-      hipHostMalloc((void **)&kv->host_ctl, 2 * sizeof(DecodeCtl), hipHostMallocDefault) != hipSuccess) {
+      hipHostMalloc((void **)&kv->host_ctl, 2 * sizeof(DecodeCtl) + 64, hipHostMallocDefault) != hipSuccess) {
     delete kv;
     return set_error(ITTS_E_DEVICE, "KV cache allocation of %zu bytes failed", 2 * n * es);
   }
@@ -1508,8 +1516,14 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     (void)hipEventDestroy(ev[0]);
     (void)hipEventDestroy(ev[1]);
   };
-  auto launch_batch = [&](int which) -> hipError_t {
-    if (use_graph && kv->persist) {
+  // Batch nb holds min(batch, max_steps - nb * batch) iterations that can sample; a shorter
+  // last batch (a short generation, the time to the first token) is launched iteration by
+  // iteration rather than as the whole graph, whose surplus iterations would only exit.
+  auto launch_batch = [&](int which, int iters) -> hipError_t {
+    if (iters < batch) {
+      for (int i = 0; i < iters; i++)
+        if (enqueue_iteration() != ITTS_OK) return hipErrorLaunchFailure;
+    } else if (use_graph && kv->persist) {
       if (persist_chained(gpt, [&] { return hipGraphLaunch(kv->gexec, gpt->stream); }) != ITTS_OK)
         return hipErrorLaunchFailure;
     } else {
@@ -1530,12 +1544,13 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
   // Each iteration samples once and `done` is set by step max_steps-1 at the latest, so
   // ceil(max_steps / batch) batches always reach the end.
   const int nb_total = (max_steps + batch - 1) / batch;
+  auto iters_of = [&](int b) { return std::min(batch, max_steps - b * batch); };
   int nb = 0;
-  hipError_t e = launch_batch(0);
+  hipError_t e = launch_batch(0, iters_of(0));
   nb = 1;
   for (int i = 0; e == hipSuccess; i++) {
     if (nb < nb_total) {
-      e = launch_batch(nb & 1);
+      e = launch_batch(nb & 1, iters_of(nb));
       nb++;
       if (e != hipSuccess) break;
     }
@@ -1543,13 +1558,18 @@ itts_status itts_generate_codes_after(itts_gpt *gpt, itts_kv *kv, const itts_cod
     if (e != hipSuccess) break;
     if (slot[i & 1]->done || i + 1 >= nb_total) break;
   }
+  // the end event, the error word and the final control block, then one synchronisation
+  // (every batch's copy into the slots has completed by then)
   if (e == hipSuccess) e = hipEventRecord(kv->ev_t[2], gpt->stream);
+  if (e == hipSuccess) e = persist_err_enqueue(kv);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(slot[0], kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost, gpt->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(gpt->stream);
   cleanup();
   HIP_TRY(e);
-  if (itts_status pst = check_persist(kv)) return pst;
+  if (itts_status pst = persist_err_check(kv)) return pst;
   DecodeCtl fin{};
-  HIP_TRY(hipMemcpy(&fin, kv->ctl.p, offsetof(DecodeCtl, seen), hipMemcpyDeviceToHost));
+  memcpy(&fin, slot[0], offsetof(DecodeCtl, seen));
   if (!fin.done) return set_error(ITTS_E_INTERNAL, "generation did not reach its end");
   kv->valid_len = fin.valid_len;
   HIP_TRY(hipEventElapsedTime(&kv->timing.prefill_ms, kv->ev_t[0], kv->ev_t[1]));
