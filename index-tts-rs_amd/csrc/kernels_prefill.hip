@@ -98,6 +98,25 @@ __device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
 
+// Loads and stores through the global address space (pointers reaching the kernel through
+// argument structs are generic to the compiler, and generic accesses count against the
+// LDS counter too).
+template <class T>
+__device__ __forceinline__ T gload(const T *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+template <class T>
+__device__ __forceinline__ void gstore(T *p, T v) {
+  *(__attribute__((address_space(1))) T *)p = v;
+}
+__device__ __forceinline__ void gstore(uint4 *p, uint4 v) {
+  *(__attribute__((address_space(1))) u32x4 *)p = u32x4{v.x, v.y, v.z, v.w};
+}
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void gstore(float2 *p, float2 v) {
+  *(__attribute__((address_space(1))) f32x2v *)p = f32x2v{v.x, v.y};
+}
+
 struct Tile {
   int tn, tm, ks;
 };
@@ -415,6 +434,31 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     if (fin) __syncthreads();  // rows reduced by one wave are read by the others
   }
 
+  // Residual epilogues on 64-row tiles: the lane's old rows y, all loaded before any is
+  // used.  Read and written element by element, each load waited behind the previous
+  // element's store (the compiler cannot move a load of y above a store to y): 16 round
+  // trips a lane.
+  constexpr bool kResid = EPI == kEpiResid;
+  float yv[kResid ? TM : 1][kResid ? TN : 1][kResid ? 16 : 1];
+  auto load_y = [&]() __attribute__((always_inline)) {
+    if constexpr (kResid) {
+#pragma unroll
+      for (int i2 = 0; i2 < TM; i2++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          // indexes clamped rather than loads predicated: one straight run of loads, which
+          // the compiler's wait counting follows exactly (behind branches it waits for every
+          // access in flight, the stores of earlier elements included)
+          const int n = min(n0 + wn * 32 * TN + j * 32 + (lane & 31), N - 1);
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const int m = min(m0 + wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), M - 1);
+            yv[i2][j][e] = gload<float>(a.y + (size_t)m * N + n);
+          }
+        }
+    }
+  };
+
   const int tile = t.tm * nN + t.tn;
   if (S > 1) {
     // Partial tiles in the MFMA register order (8 bytes per access, contiguous across the
@@ -448,6 +492,9 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     if (tid == 0) last_flag = atomicInc(a.cnt + tile, (uint32_t)(S - 1)) == (uint32_t)(S - 1) ? 1u : 0u;
     __syncthreads();
     if (!last_flag) return;
+    // (the old rows' loads go out ahead of the partials', their latencies overlapping; on
+    // 128-row tiles, whose registers are full here, after them)
+    if (kResid && TM == 1 && worker) load_y();
     // splits added in split order (the block's own partial from registers)
     if (worker) {
 #pragma unroll
@@ -482,6 +529,8 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
     }
   }
 
+  if (kResid && S == 1 && TM == 1 && worker) load_y();
+
   if constexpr (EPI == kEpiResid) {
     if (a.tfo.st) {
       // The updated rows x staged in LDS, then per (row, 64-column group): the group's mean
@@ -492,17 +541,21 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       static_assert(ITEMS * TPI == 256 && VPT % 8 == 0, "fold epilogue shape");
       float *T = reinterpret_cast<float *>(lds);
       // this thread's item (row rl, 64-column group grp, values c0 .. c0 + VPT - 1); its
-      // gamma values are loaded first, under the staging below (16-byte aligned: the
-      // vector starts on 256 bytes and c0 is a multiple of 16)
+      // gamma values (16-byte aligned: the vector starts on 256 bytes and c0 is a multiple
+      // of 16) are loaded under the staging below on 64-row tiles, after it on 128-row
+      // tiles (whose registers the staged tile still holds)
       const int item = tid / TPI, sub = tid % TPI;
       const int rl = item / GPR, grp = item % GPR;
       const int c0 = grp * 64 + sub * VPT;
       // N is a multiple of 64: a group is wholly in or out
       const bool live = worker && m0 + rl < M && n0 + c0 < N;
       float4 gam[VPT / 4];
+      auto load_gamma = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int c = 0; c < VPT / 4; c++)
-        gam[c] = live ? reinterpret_cast<const float4 *>(a.tfo.gamma + n0 + c0)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < VPT / 4; c++)
+          gam[c] = live ? reinterpret_cast<const float4 *>(a.tfo.gamma + n0 + c0)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      };
+      if constexpr (TM == 1) load_gamma();
       __syncthreads();
       if (worker)
 #pragma unroll
@@ -512,17 +565,26 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
             const int cl = wn * 32 * TN + j * 32 + (lane & 31), n = n0 + cl;
             if (n >= N) continue;
             const float bias = a.ql.bias[n];
+            const int rb = wm * 32 * TM + i2 * 32 + (lane >> 5) * 4;  // tile row of element 0
+            // values first (straight-line), then the stores predicated on the row
+            float outv[16];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-              const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-              const int m = m0 + rl;
-              if (m >= M) continue;
-              const float v = a.y[(size_t)m * N + n] + (acc[i2][j][e] + bias);
-              a.y[(size_t)m * N + n] = v;
-              T[rl * LDT + cl] = v;
+              const float y = TM == 1 ? yv[i2][j][e]
+                                      : gload(a.y + (size_t)min(m0 + rb + (e >> 2) * 8 + (e & 3), M - 1) * N + n);
+              outv[e] = y + (acc[i2][j][e] + bias);
+              T[(rb + (e >> 2) * 8 + (e & 3)) * LDT + cl] = outv[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) asm volatile("" : "+v"(outv[e]));
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+              const int m = m0 + rb + (e >> 2) * 8 + (e & 3);
+              if (m < M) gstore(a.y + (size_t)m * N + n, outv[e]);
             }
           }
       __syncthreads();
+      if constexpr (TM != 1) load_gamma();
       if (worker) {
         const int m = m0 + rl, n = n0 + c0;
         float xv[VPT];
@@ -556,16 +618,16 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
             lw[e >> 1] = l0 | (l1 << 16);
           }
           if (live) {
-            *reinterpret_cast<uint4 *>(a.tfo.o.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            *reinterpret_cast<uint4 *>(a.tfo.o.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            gstore(reinterpret_cast<uint4 *>(a.tfo.o.hi + (size_t)m * N + n + c), make_uint4(hw[0], hw[1], hw[2], hw[3]));
+            gstore(reinterpret_cast<uint4 *>(a.tfo.o.lo + (size_t)m * N + n + c), make_uint4(lw[0], lw[1], lw[2], lw[3]));
           }
         }
         m2 = item_sum<TPI>(m2);
         gsum = item_sum<TPI>(gsum);
         if (live && sub == 0) {
           const size_t gi = (size_t)m * (N / kGroup) + (n0 + grp * 64) / kGroup;
-          a.tfo.o.gs[gi] = gsum;
-          a.tfo.st[gi] = make_float2(mean, m2);
+          gstore(a.tfo.o.gs + gi, gsum);
+          gstore(a.tfo.st + gi, make_float2(mean, m2));
         }
       }
       return;
@@ -620,12 +682,12 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
           lw[e >> 1] = l0 | (l1 << 16);
         }
         if (live) {
-          *reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-          *reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+          gstore(reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c), make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          gstore(reinterpret_cast<uint4 *>(a.xo.lo + (size_t)m * N + n + c), make_uint4(lw[0], lw[1], lw[2], lw[3]));
         }
       }
       sum = item_sum<TPI>(sum);
-      if (live && sub == 0) a.xo.gs[(size_t)m * (N / kGroup) + n / kGroup] = sum;
+      if (live && sub == 0) gstore(a.xo.gs + (size_t)m * (N / kGroup) + n / kGroup, sum);
     }
     return;
   } else if (worker) {
@@ -637,39 +699,77 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
         if (n >= N) continue;
         const float bias = fin ? a.tfi.c[n] : a.ql.bias[n];
         const float gn = fin ? a.tfi.G[n] : 0.0f;
+        const int rb = wm * 32 * TM + i2 * 32 + (lane >> 5) * 4;  // tile row of element 0
+        // 128-row tiles: the sub-tile's 16 old values loaded together (registers for all 64
+        // of the lane's would spill)
+        float ysub[kResid && TM != 1 ? 16 : 1];
+        if constexpr (kResid && TM != 1) {
+#pragma unroll
+          for (int e = 0; e < 16; e++)
+            ysub[e] = gload(a.y + (size_t)min(m0 + rb + (e >> 2) * 8 + (e & 3), M - 1) * N + n);
+        }
+        // The sub-tile's values first, in straight-line code (the waits on its loads come
+        // here, once), then the stores, each predicated on its row: behind a predicate the
+        // compiler's wait counting waits for every access in flight, earlier stores too.
+        float outv[16];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          const int m = m0 + rl;
-          if (m >= M) continue;
+          const int rl = rb + (e >> 2) * 8 + (e & 3);
           float v = acc[i2][j][e];
-          if (fin) v = fold_row[rl].y * (v - fold_row[rl].x * gn);
+          if constexpr (kFoldIn) v = fin ? fold_row[rl].y * (v - fold_row[rl].x * gn) : v;
           v += bias;
-          if constexpr (EPI == kEpiStore) {
-            a.y[(size_t)m * N + n] = v;
-          } else if constexpr (EPI == kEpiResid) {
-            a.y[(size_t)m * N + n] += v;
+          if constexpr (kResid) v = (TM == 1 ? yv[i2][j][e] : ysub[e]) + v;
+          outv[e] = v;
+        }
+        // (an empty asm over the values keeps the compiler from sinking their arithmetic,
+        // and the waits on its operands, into the predicated stores)
+#pragma unroll
+        for (int e = 0; e < 16; e++) asm volatile("" : "+v"(outv[e]));
+        // stores through the global address space (generic stores also count against the
+        // LDS counter)
+        if constexpr (EPI == kEpiStore || EPI == kEpiResid) {
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const int m = m0 + rb + (e >> 2) * 8 + (e & 3);
+            if (m < M) gstore(a.y + (size_t)m * N + n, outv[e]);
+          }
+        } else {
+          const int d = a.qkv.d_model;
+          if (n < d) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+              const int m = m0 + rb + (e >> 2) * 8 + (e & 3);
+              if (m < M) gstore(a.qkv.q_out + (size_t)m * d + n, outv[e]);
+            }
           } else {
-            const int d = a.qkv.d_model;
-            if (n < d) {
-              a.qkv.q_out[(size_t)m * d + n] = v;
-            } else {
-              const int idx = n < 2 * d ? n - d : n - 2 * d;
-              const int h = idx >> 6, e2 = idx & 63;
-              void *cache = n < 2 * d ? a.qkv.k_cache : a.qkv.v_cache;
-              int pos = a.qkv.pos0 + m;
-              if (a.qkv.seqs) {  // batched decode: row m is sequence m
-                const BatchSeq &sq = a.qkv.seqs[m];
-                if (sq.ctl->done) continue;
-                pos = sq.ctl->valid_len;
-                cache = static_cast<char *>(n < 2 * d ? sq.k : sq.v) +
-                        a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4);
-              }
+            const bool is_k = n < 2 * d;
+            const int idx = is_k ? n - d : n - 2 * d;
+            const int h = idx >> 6, e2 = idx & 63;
+            auto put = [&](void *cache, int pos, float v) __attribute__((always_inline)) {
               const size_t ci = ((size_t)h * a.qkv.max_seq + pos) * kHeadDim + e2;
               if constexpr (KVT == kKvBf16) {
-                static_cast<uint16_t *>(cache)[ci] = (uint16_t)float_to_bf16_bits(v);
+                gstore(static_cast<uint16_t *>(cache) + ci, (uint16_t)float_to_bf16_bits(v));
               } else {
-                static_cast<float *>(cache)[ci] = v;
+                gstore(static_cast<float *>(cache) + ci, v);
+              }
+            };
+            if (!a.qkv.seqs) {
+              void *cache = is_k ? a.qkv.k_cache : a.qkv.v_cache;
+#pragma unroll
+              for (int e = 0; e < 16; e++) {
+                const int m = m0 + rb + (e >> 2) * 8 + (e & 3);
+                if (m < M) put(cache, a.qkv.pos0 + m, outv[e]);
+              }
+            } else {  // batched decode: row m is sequence m
+#pragma unroll
+              for (int e = 0; e < 16; e++) {
+                const int m = m0 + rb + (e >> 2) * 8 + (e & 3);
+                if (m >= M) continue;
+                const BatchSeq *sq = a.qkv.seqs + m;
+                DecodeCtl *ctl = gload(&sq->ctl);
+                if (gload<int32_t>(&ctl->done)) continue;
+                put(static_cast<char *>(gload(is_k ? &sq->k : &sq->v)) + a.qkv.layer_off * (KVT == kKvBf16 ? 2 : 4),
+                    gload<int32_t>(&ctl->valid_len), outv[e]);
               }
             }
           }
