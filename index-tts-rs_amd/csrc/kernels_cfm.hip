@@ -538,13 +538,24 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   if (kg == 1 || c >= N) return;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] += red[i * 64];
+  // With beta, the old outputs are loaded together (rows clamped, not predicated) and the
+  // new values formed before the row-predicated stores: read and written element by
+  // element, each load would wait behind the previous element's store.
+  const int rb = m0 + wm * 32 + (lane >> 5) * 4;  // row of element 0
+  if (beta != 0.0f) {
+    float old[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) old[i] = y[(size_t)min(rb + (i >> 2) * 8 + (i & 3), M - 1) * ldy + c];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      acc[i] = acc[i] + beta * old[i];
+      asm volatile("" : "+v"(acc[i]));
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    const int r = m0 + wm * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-    if (r < M) {
-      float *o = y + (size_t)r * ldy + c;
-      *o = beta == 0.0f ? acc[i] : acc[i] + beta * *o;
-    }
+    const int r = rb + (i >> 2) * 8 + (i & 3);
+    if (r < M) y[(size_t)r * ldy + c] = acc[i];
   }
 }
 

@@ -408,24 +408,28 @@ __device__ __forceinline__ int32_t sample_block(const float *src, float *penalis
 
 // generate_codes_after's bookkeeping after sample s (sampler.rs:378-388): STOP ends the
 // generation; otherwise the code is emitted, marked seen, and becomes the next step's token
-// at position n_prior + s + 2 unless s was the last step.  Thread 0 only.
+// at position n_prior + s + 2 unless s was the last step.  Thread 0 only.  Every field is
+// read before the first store: read between the stores (which the compiler cannot prove
+// apart from them), each read would wait for the stores before it.
 __device__ inline void sampler_commit(DecodeCtl *c, uint64_t *seen, int32_t result, int stop_tok, int32_t *codes) {
+  const int n_codes = c->n_codes, s = c->step, max_steps = c->max_steps, n_prior = c->n_prior;
+  const bool stop = result == stop_tok, mark = !stop && result >= 0 && result < kSeenWords * 64;
+  const uint64_t word = mark ? seen[result >> 6] : 0ull;
   c->last_tok = result;
-  if (result == stop_tok) {
+  if (stop) {
     c->done = 1;
   } else {
-    codes[c->n_codes] = result;
-    c->n_codes += 1;
-    if (result >= 0 && result < kSeenWords * 64) seen[result >> 6] |= 1ull << (result & 63);
-    const int s = c->step;
-    if (s + 1 < c->max_steps) {
+    codes[n_codes] = result;
+    c->n_codes = n_codes + 1;
+    if (mark) seen[result >> 6] = word | (1ull << (result & 63));
+    if (s + 1 < max_steps) {
       c->tok = result;
-      c->pos = c->n_prior + s + 2;
+      c->pos = n_prior + s + 2;
     } else {
       c->done = 1;
     }
   }
-  c->step += 1;
+  c->step = s + 1;
 }
 
 }  // namespace itts
