@@ -506,13 +506,33 @@ __device__ __forceinline__ void ln_stats(const float *x, int n, float *st, uint3
 // Layer l: [ln_1 gamma d][ln_2 gamma d] and the block's rows of c_qkv, G_qkv, the c_proj
 // bias, c_fc, G_fc and the mlp c_proj bias (folded LayerNorms: the betas live in c).
 // l == n_layer (the head): [ln_f w][ln_f b][final_norm w][final_norm b][mel_head bias rows].
+// Global -> LDS copies issued by hand (lane l's bytes land at lds + l * size, lds in M0).
+// Issued with the builtin, every copy waited for the one before it to land: the compiler
+// cannot tell apart the LDS bytes a pending copy writes and waits for it before the next
+// access to LDS, the next copy included.  The publisher's own s_waitcnt covers them before
+// their LDS rows are read.  M0 is set before every copy (and declared clobbered).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void pub_dma16(const void *src, const float *lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void pub_dma4(const void *src, const float *lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, float *lp, const RowMap &mq,
                                                  const RowMap &mp, const RowMap &mf, const RowMap &mm,
                                                  const RowMap &mh, int lane) {
-  typedef __attribute__((address_space(3))) void *lds_ptr;
   const int d = a.d;
   const bool head = l >= a.n_layer;
-  const DevLayer *Ly = head ? nullptr : a.layers + l;
+  // the layer's pointers by scalar loads (the constant address space): by vector loads
+  // the copies' own source pointers would wait for every copy issued before them, since
+  // vector loads complete in issue order
+  typedef const __attribute__((address_space(4))) DevLayer ConstLayer;
+  ConstLayer *Ly = head ? nullptr : (ConstLayer *)(a.layers) + l;
   const int nv = head ? 4 : 2;
 #pragma unroll
   for (int arr = 0; arr < 4; arr++) {
@@ -520,12 +540,12 @@ __device__ __forceinline__ void stage_params_dma(const PersistArgs &a, int l, fl
     const float *src = head ? (arr == 0 ? a.ln_f_w : arr == 1 ? a.ln_f_b : arr == 2 ? a.fn_w : a.fn_b)
                             : (arr == 0 ? Ly->ln1_w : Ly->ln2_w);
     for (int off = 0; off < d; off += 256)  // 64 lanes x 4 floats per copy
-      if (off + lane * 4 < d) __builtin_amdgcn_global_load_lds(src + off + lane * 4, (lds_ptr)(lp + arr * d + off), 16, 0, 0);
+      if (off + lane * 4 < d) pub_dma16(src + off + lane * 4, lp + arr * d + off);
   }
   float *bl = lp + nv * d;
   auto rows = [&](const RowMap &m, const float *v) {
     for (int r0 = 0; r0 < m.rows; r0 += 64)
-      if (r0 + lane < m.rows) __builtin_amdgcn_global_load_lds(v + m.row0 + r0 + lane, (lds_ptr)(bl + r0), 4, 0, 0);
+      if (r0 + lane < m.rows) pub_dma4(v + m.row0 + r0 + lane, bl + r0);
     bl += m.rows;
   };
   if (head) {
