@@ -725,6 +725,10 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (sh.abort) return;
     if (poller) ln_stats(xin, d, sh.red, &sh.stat_cnt, T);
     if (loader) dot_slots<BITS>(wq, m_qkv, xn, part, ll);
+    // this layer's c_proj slice (layer 0's came with the prologue), issued once the QKV dot
+    // has its codes: 511.8 against 513.6 us per step with it issued after the previous
+    // layer's x publish
+    if (loader && l > 0) load_slots<BITS, PT>(wp, Ly.proj, m_proj, ll);
     __syncthreads();
     if (loader) {
       const float mu = sh.red[24], rstd = sh.red[25];
@@ -1084,10 +1088,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
       });
     __syncthreads();
     if (pub) publish_rows(a.x_x, d, B, b, out, m_mp.rows, ep + 6u, lane);
-    // the next layer's c_proj slice (its registers are free once this layer's c_proj is
-    // done), issued after the phase's exchange stores (barrier: 535 against 547 us)
     __syncthreads();
-    if (loader && l + 1 < a.n_layer) load_slots<BITS, PT>(wp, a.layers[l + 1].proj, m_proj, ll);
   }
   // ---------------- head: ln_f, final_norm, mel_head rows -> logits ------------------
   {
