@@ -283,13 +283,17 @@ __device__ inline const void *head_base(const void *c, size_t off) {
 template <int KVT>
 struct Row8 {
   uint32_t w[KVT == kKvBf16 ? 4 : 8];
+  // through the global address space: a cache pointer read from a sequence descriptor is
+  // generic to the compiler, and generic (flat) loads also count against the LDS counter
+  typedef unsigned int gu32x4 __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) gu32x4 *gptr;
   __device__ __forceinline__ void load(const void *base, size_t row, int c0) {
     if constexpr (KVT == kKvBf16) {
-      const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(base) + row * 64 + c0);
+      const gu32x4 u = *(gptr)(static_cast<const uint16_t *>(base) + row * 64 + c0);
       w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
     } else {
-      const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const float *>(base) + row * 64 + c0);
-      const uint4 u0 = p[0], u1 = p[1];
+      const gptr p = (gptr)(static_cast<const float *>(base) + row * 64 + c0);
+      const gu32x4 u0 = p[0], u1 = p[1];
       w[0] = u0.x; w[1] = u0.y; w[2] = u0.z; w[3] = u0.w;
       w[4] = u1.x; w[5] = u1.y; w[6] = u1.z; w[7] = u1.w;
     }
