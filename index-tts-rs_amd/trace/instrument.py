@@ -40,7 +40,7 @@ once("// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache --
      "// ---------------- P1: LN1 (folded), QKV rows; K/V rows into the cache ------------\n    STAMP(0);\n"
      "    if (T == 0 && l == g_trace_layer && b < 1024) g_trace[b][24] = __builtin_amdgcn_s_memtime();")
 stamp_after(r"\] = lp\[i\] \* xin\[i\];\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 1)
-stamp_after(r"dot_slots<BITS>\(wq, m_qkv, xn, part, ll\);\s*__syncthreads\(\);", 2)
+stamp_after(r"dot_slots<BITS>\(wq, m_qkv, xn, part, ll\);(?:\s*//[^\n]*)*\s*if \(loader && l > 0\) load_slots<BITS, PT>\(wp, Ly\.proj, m_proj, ll\);\s*__syncthreads\(\);", 2)
 stamp_after(r"lp\[bo_cq \+ r\]; \}\);\s*\}\s*__syncthreads\(\);", 3)
 stamp_after(r"if \(!ok\) sh\.abort = 1;\s*\}\s*__syncthreads\(\);\s*if \(sh\.abort\) return;", 4)
 stamp_after(r"if \(lane == 0\) sh\.m_w\[lw\] = mloc;\s*\}\s*__syncthreads\(\);", 5)
