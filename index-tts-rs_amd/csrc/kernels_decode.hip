@@ -554,7 +554,8 @@ __device__ inline void put_split(const SplitOut &o, size_t i, size_t gi, float v
 
 // Prefill attention, one wave per (head, row) over the row's keys in series.  (Four waves
 // a row, its tiles side by side and merged in LDS (attn_row_merged), made the 235-row
-// prefill 2.36 -> 2.44 ms: the short rows' idle waves cost more than the long rows gain.)
+// prefill 2.36 -> 2.44 ms: the short rows' idle waves cost more than the long rows gain;
+// two waves a row measured no faster.)
 template <int KVT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
                                                           const void *vc, int max_seq, int d,
