@@ -40,6 +40,37 @@ def _prompts(W, specs, seed0):
 
 
 @pytest.mark.parametrize("kvt", [H.ITTS_BF16, H.ITTS_F32])
+def test_step_batch_ten_sequences(small, kvt):
+    """More than 8 rows: the tiled products (LayerNorm row kernels, the QKV epilogue's
+    per-sequence K/V scatter read from the sequence descriptors) instead of the few-row
+    ones, each sequence against the oracle stepping it alone."""
+    W, g, M = small
+    say(f"[gpu] step_batch of 10 kv={kvt}")
+    specs = [(4 + 7 * i, (5 * i) % 13, i % 4) for i in range(10)]
+    ps = _prompts(W, specs, 40)
+    caches, okvs = [], []
+    for pr, prior, lang in ps:
+        kv = g.kv_cache(256, kvt)
+        okv = M.kv(256, kv_bf16=kvt == H.ITTS_BF16)
+        g.prefill_after(pr.text_tokens, pr.conds, lang, prior, kv, logits=False)
+        M.prefill_after(okv, pr.text_tokens, pr.conds, lang, prior)
+        caches.append(kv)
+        okvs.append(okv)
+    rng = np.random.default_rng(3)
+    for step in range(3):
+        toks = rng.integers(0, 1000, len(ps)).astype(np.int32)
+        pos = np.array([len(prior) + 2 + step for _, prior, _ in ps], np.int32)
+        got = H.step_batch(g, caches, toks, pos)
+        for b, okv in enumerate(okvs):
+            ref = M.step(okv, int(toks[b]), int(pos[b]))
+            assert np.abs(got[b] - ref).max() < TIGHT, (step, b)
+            assert caches[b].valid_len() == okv.valid_len()
+    for l in range(W.cfg["n_layer"]):
+        for b in (0, 9):
+            assert np.allclose(caches[b].read(l, 1), okvs[b].read(l, 1), rtol=1e-2, atol=1e-4)
+
+
+@pytest.mark.parametrize("kvt", [H.ITTS_BF16, H.ITTS_F32])
 def test_step_batch_matches_oracle_per_sequence(small, kvt):
     W, g, M = small
     say(f"[gpu] step_batch kv={kvt}")
