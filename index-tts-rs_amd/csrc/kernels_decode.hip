@@ -324,35 +324,27 @@ __device__ __forceinline__ float row_score(const float4 &qa, const float4 &qb, c
   return t * 0.125f;
 }
 
-// One wave: online-softmax attention of query q over keys j0..j1-1 (prefill rows), 64 keys
-// a tile.  Lane = (key group kg = lane / 8, dims 8 (lane % 8) .. +7): a lane holds keys
-// kg, kg + 8, .. of the tile, K and V rows both spread over eight adjacent lanes (16 bytes
-// each, so a load instruction reads eight whole rows) and all of a tile's loads are in
-// flight at once; probabilities stay in the lane that holds the key, and the eight key
-// groups are added once at the end.  o returns dimension `lane`.
+// One wave's online-softmax state over one query row, 64 keys a tile.  Lane = (key group
+// kg = lane / 8, dims 8 (lane % 8) .. +7): a lane holds keys kg, kg + 8, .. of the tile, K and
+// V rows both spread over eight adjacent lanes (16 bytes each, so a load instruction reads
+// eight whole rows); probabilities stay in the lane that holds the key, and the eight key
+// groups are added once at the end (finish: dimension `lane` of the unnormalised output).
 template <int KVT>
-__device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
-                                  float &m, float &l, float &o) {
-  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
-  const float4 qa = reinterpret_cast<const float4 *>(q)[2 * dc], qb = reinterpret_cast<const float4 *>(q)[2 * dc + 1];
-  m = -INFINITY;
-  l = 0.0f;
-  float acc[8];
+struct AttnRun {
+  float4 qa, qb;
+  float m, l, acc[8];
+  __device__ __forceinline__ void init(const float *q) {
+    const int dc = threadIdx.x & 7;
+    qa = reinterpret_cast<const float4 *>(q)[2 * dc];
+    qb = reinterpret_cast<const float4 *>(q)[2 * dc + 1];
+    m = -INFINITY;
+    l = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-  for (int t0 = j0; t0 < j1; t0 += 64) {
-    Row8<KVT> kr[8], vr[8];
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const int key = t0 + kg + 8 * jj;
-      if (key < j1) {
-        kr[jj].load(kh, (size_t)key, dc * 8);
-        vr[jj].load(vh, (size_t)key, dc * 8);
-      } else {
-        kr[jj].zero();
-        vr[jj].zero();
-      }
-    }
+    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+  }
+  // keys t0 .. min(t0 + 64, j1) - 1, rows kr/vr as this lane holds them (zero past j1)
+  __device__ __forceinline__ void tile(int t0, int j1, const Row8<KVT> (&kr)[8], const Row8<KVT> (&vr)[8]) {
+    const int kg = (threadIdx.x & 63) >> 3;
     float sc[8], mt = -INFINITY;
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
@@ -380,20 +372,52 @@ __device__ inline void attn_range(const float *q, const void *kh, const void *vh
     l = l * corr + ps;
     m = mn;
   }
-  // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits in
-  // element lane % 8 of lane lane / 8
+  __device__ __forceinline__ float finish() {
+    const int lane = threadIdx.x & 63, dc = lane & 7;
+    // add the eight key groups (lanes dc, dc + 8, .., dc + 56), then dimension `lane` sits
+    // in element lane % 8 of lane lane / 8
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    acc[e] += dpp_pair<0x128>(acc[e]);  // row_ror:8 = lane ^ 8
-    acc[e] += swizzle_xor16(acc[e]);
-    acc[e] += __shfl_xor(acc[e], 32, 64);
-  }
-  o = 0.0f;
+    for (int e = 0; e < 8; e++) {
+      acc[e] += dpp_pair<0x128>(acc[e]);  // row_ror:8 = lane ^ 8
+      acc[e] += swizzle_xor16(acc[e]);
+      acc[e] += __shfl_xor(acc[e], 32, 64);
+    }
+    float o = 0.0f;
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float x = __shfl(acc[e], lane >> 3, 64);
-    if (dc == e) o = x;
+    for (int e = 0; e < 8; e++) {
+      const float x = __shfl(acc[e], lane >> 3, 64);
+      if (dc == e) o = x;
+    }
+    return o;
   }
+};
+
+// One wave: attention of query q over keys j0..j1-1, the tiles' K and V rows loaded from
+// the cache (all of a tile's loads in flight at once).  o returns dimension `lane`.
+template <int KVT>
+__device__ inline void attn_range(const float *q, const void *kh, const void *vh, int j0, int j1,
+                                  float &m, float &l, float &o) {
+  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
+  AttnRun<KVT> run;
+  run.init(q);
+  for (int t0 = j0; t0 < j1; t0 += 64) {
+    Row8<KVT> kr[8], vr[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int key = t0 + kg + 8 * jj;
+      if (key < j1) {
+        kr[jj].load(kh, (size_t)key, dc * 8);
+        vr[jj].load(vh, (size_t)key, dc * 8);
+      } else {
+        kr[jj].zero();
+        vr[jj].zero();
+      }
+    }
+    run.tile(t0, j1, kr, vr);
+  }
+  o = run.finish();
+  m = run.m;
+  l = run.l;
 }
 
 struct AttnShared {
@@ -552,23 +576,99 @@ __device__ inline void put_split(const SplitOut &o, size_t i, size_t gi, float v
   if ((threadIdx.x & 63) == 0) o.gs[gi] = s;
 }
 
-// Prefill attention, one wave per (head, row) over the row's keys in series.  (Four waves
-// a row, its tiles side by side and merged in LDS (attn_row_merged), made the 235-row
-// prefill 2.36 -> 2.44 ms: the short rows' idle waves cost more than the long rows gain;
-// two waves a row measured no faster.)
+// Global -> LDS copies issued by hand (lane l's 16 bytes land at lds + 16 l, lds in M0):
+// issued with the builtin, the compiler would wait for every copy in flight before each LDS
+// read; here the kernel's own s_waitcnt counts them.  M0 is set before every copy.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void attn_dma16(const void *src, const void *lds) {
+  // the destination is the same for the whole wave (the callers' addresses are uniform)
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Prefill attention with the key tiles shared: one block of kPrefillRows waves per (head,
+// kPrefillRows consecutive rows), wave w on row 4g + w.  Each 64-key tile of K and V is
+// copied into LDS once (double-buffered, the next tile's copies in flight during this
+// tile) and read by every wave from there, where a wave per row would read it from L2 once
+// per row.  The tile arithmetic is AttnRun's, on the same rows, so each row's result is the
+// one attn_range gives.  Measured at a 235-row prefill: 2.15-2.19 -> 2.11-2.13 ms against a
+// wave per (head, row) reading its keys itself; 8 rows a block no faster; a row's tiles
+// over 2 or 4 waves merged in LDS (attn_row_merged) no faster or slower (2.36 -> 2.44 ms).
+constexpr int kPrefillRows = 4;
 template <int KVT>
-__global__ __launch_bounds__(64) void attn_prefill_kernel(const float *q, int base, const void *kc,
-                                                          const void *vc, int max_seq, int d,
-                                                          SplitOut out) {
-  // rows in reverse order, so the longest key ranges are dispatched first and the short
-  // ones fill in behind them
-  const int h = blockIdx.x, t = gridDim.y - 1 - blockIdx.y;
+__global__ __launch_bounds__(64 * kPrefillRows) void attn_prefill_tiles_kernel(const float *q, int T, int base,
+                                                                               const void *kc, const void *vc,
+                                                                               int max_seq, int d, SplitOut out) {
+  constexpr int ES = KVT == kKvBf16 ? 2 : 4;         // bytes per element
+  constexpr int RB = 64 * ES, TB = 64 * RB;          // bytes per cache row, per 64-key tile
+  constexpr int PIECES = TB / 16 / (64 * kPrefillRows);  // 16-byte copies per thread per tile and matrix
+  __shared__ __attribute__((aligned(16))) char kv_lds[2][2][TB];  // [buffer][K, V][tile]
+  // groups in reverse order, so the longest key ranges are dispatched first
+  const int h = blockIdx.x, g = gridDim.y - 1 - blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, kg = lane >> 3, dc = lane & 7;
+  const int t = kPrefillRows * g + wave;
+  const int tl = min(t, T - 1);  // a wave past the last row runs that row and stores nothing
+  const int L = base + tl + 1, Lb = base + min(kPrefillRows * g + kPrefillRows, T);
   const size_t hb = (size_t)h * max_seq * 64;
-  float m, l, o;
-  attn_range<KVT>(q + (size_t)t * d + h * 64, head_base<KVT>(kc, hb), head_base<KVT>(vc, hb), 0, base + t + 1,
-                  m, l, o);
-  // one head is one 64-column group of the c_proj input
-  put_split(out, (size_t)t * d + h * 64 + threadIdx.x, (size_t)t * (d / 64) + h, o / l);
+  const char *kb = static_cast<const char *>(head_base<KVT>(kc, hb));
+  const char *vb = static_cast<const char *>(head_base<KVT>(vc, hb));
+  const int ntile = (Lb + 63) / 64;
+  // tile i into buffer i & 1: piece p = j * (64 kPrefillRows) + threadIdx.x of each matrix,
+  // rows past the cache's end read its last row (never used: those keys are past every row)
+  auto copy = [&](int i) {
+#pragma unroll
+    for (int j = 0; j < PIECES; j++) {
+      const int pc = j * 64 * kPrefillRows + (int)threadIdx.x, row = pc * 16 / RB;
+      const size_t off = (size_t)min(64 * i + row, max_seq - 1) * RB + (pc * 16) % RB;
+      const int dst = (j * 64 * kPrefillRows + wave * 64) * 16;  // the wave's 1 KB, uniform
+      attn_dma16(kb + off, &kv_lds[i & 1][0][dst]);
+      attn_dma16(vb + off, &kv_lds[i & 1][1][dst]);
+    }
+  };
+  AttnRun<KVT> run;
+  run.init(q + (size_t)tl * d + h * 64);
+  copy(0);
+  for (int i = 0; i < ntile; i++) {
+    if (i + 1 < ntile) {
+      copy(i + 1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PIECES) : "memory");  // tile i's copies
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    if (64 * i < L) {  // wave-uniform: the row's keys reach this tile
+      Row8<KVT> kr[8], vr[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) {
+        const int r = kg + 8 * jj;
+        if (64 * i + r < L) {
+          const uint4 *pk = reinterpret_cast<const uint4 *>(&kv_lds[i & 1][0][r * RB + dc * 8 * ES]);
+          const uint4 *pv = reinterpret_cast<const uint4 *>(&kv_lds[i & 1][1][r * RB + dc * 8 * ES]);
+          if constexpr (KVT == kKvBf16) {
+            const uint4 a = pk[0], b = pv[0];
+            kr[jj].w[0] = a.x; kr[jj].w[1] = a.y; kr[jj].w[2] = a.z; kr[jj].w[3] = a.w;
+            vr[jj].w[0] = b.x; vr[jj].w[1] = b.y; vr[jj].w[2] = b.z; vr[jj].w[3] = b.w;
+          } else {
+            const uint4 a0 = pk[0], a1 = pk[1], b0 = pv[0], b1 = pv[1];
+            kr[jj].w[0] = a0.x; kr[jj].w[1] = a0.y; kr[jj].w[2] = a0.z; kr[jj].w[3] = a0.w;
+            kr[jj].w[4] = a1.x; kr[jj].w[5] = a1.y; kr[jj].w[6] = a1.z; kr[jj].w[7] = a1.w;
+            vr[jj].w[0] = b0.x; vr[jj].w[1] = b0.y; vr[jj].w[2] = b0.z; vr[jj].w[3] = b0.w;
+            vr[jj].w[4] = b1.x; vr[jj].w[5] = b1.y; vr[jj].w[6] = b1.z; vr[jj].w[7] = b1.w;
+          }
+        } else {
+          kr[jj].zero();
+          vr[jj].zero();
+        }
+      }
+      run.tile(64 * i, L, kr, vr);
+    }
+    __syncthreads();  // buffer i & 1 is refilled with tile i + 2 next
+  }
+  const float o = run.finish();
+  if (t < T) put_split(out, (size_t)t * d + h * 64 + lane, (size_t)t * (d / 64) + h, o / run.l);
 }
 
 // Attention probe (replay, gpt.rs:391-422): softmax probabilities of head p.head for the
@@ -819,12 +919,15 @@ hipError_t launch_ln_rows(const float *x, const float *w, const float *b, int T,
 
 hipError_t launch_attn_prefill(const float *q, int T, int base, const void *kc, const void *vc,
                                int n_head, int max_seq, const SplitOut &out, int kvt, hipStream_t s) {
-  dim3 grid(n_head, T);
   const int d = n_head * 64;
+  if (T <= 0) return hipSuccess;
+  dim3 grid(n_head, (T + kPrefillRows - 1) / kPrefillRows);
   if (kvt == kKvBf16) {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvBf16>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
+    hipLaunchKernelGGL(attn_prefill_tiles_kernel<kKvBf16>, grid, dim3(64 * kPrefillRows), 0, s, q, T, base, kc, vc,
+                       max_seq, d, out);
   } else {
-    hipLaunchKernelGGL(attn_prefill_kernel<kKvF32>, grid, dim3(64), 0, s, q, base, kc, vc, max_seq, d, out);
+    hipLaunchKernelGGL(attn_prefill_tiles_kernel<kKvF32>, grid, dim3(64 * kPrefillRows), 0, s, q, T, base, kc, vc,
+                       max_seq, d, out);
   }
   return hipGetLastError();
 }
