@@ -80,6 +80,38 @@ struct DevBuf {
 };
 
 // Activation rows in the prefill GEMM's split form (bf16 hi/lo planes + group sums).
+// Pinned host staging for asynchronous uploads: the copies that read it are followed by
+// `ready`, and the next rewrite waits for that event first, so a call returns without
+// waiting for its uploads to land.
+struct HostStage {
+  void *p = nullptr;
+  size_t bytes = 0;
+  hipEvent_t ready = nullptr;
+  ~HostStage() {
+    if (ready) (void)hipEventDestroy(ready);
+    if (p) (void)hipHostFree(p);
+  }
+  // room for n bytes, once the previous uploads from here have landed
+  hipError_t acquire(size_t n) {
+    hipError_t e = ready ? hipEventSynchronize(ready) : hipEventCreateWithFlags(&ready, hipEventDisableTiming);
+    if (e != hipSuccess || n <= bytes) return e;
+    if (p) {
+      e = hipHostFree(p);
+      p = nullptr;
+      bytes = 0;
+      if (e != hipSuccess) return e;
+    }
+    e = hipHostMalloc(&p, n, hipHostMallocDefault);
+    if (e == hipSuccess) bytes = n;
+    return e;
+  }
+  hipError_t release(hipStream_t s) { return hipEventRecord(ready, s); }
+  template <class T>
+  T *as() const {
+    return static_cast<T *>(p);
+  }
+};
+
 struct SplitBuf {
   DevBuf hi, lo, gs;
   hipError_t ensure(size_t M, int K) {
@@ -155,6 +187,7 @@ struct itts_gpt {
   // prefill workspace (grown on demand): residual stream and q (fp32), GEMM inputs in
   // split form (LN output, attention output, GELU output), split-K partials and counters
   DevBuf px, pq, rows, conds;
+  HostStage h_rows, h_conds;  // their pinned host staging
   SplitBuf ph, pa, pf;
   // the folded LayerNorms' group statistics of the residual rows [M][d/64] (mean, M2)
   DevBuf pst;
@@ -366,21 +399,29 @@ itts_status embed_prompts(itts_gpt *g, const itts_code_prompt *ps, int B, std::v
   if (itts_status st = ensure_rows(g, M)) return st;
   HIP_TRY(g->rows.ensure(sizeof(EmbedRow) * (size_t)M));
   HIP_TRY(g->conds.ensure(sizeof(float) * (size_t)std::max(1, n_cond_all) * d));
-  HIP_TRY(hipMemcpyAsync(g->rows.p, rows.data(), sizeof(EmbedRow) * M, hipMemcpyHostToDevice, g->stream));
+  // through pinned staging, so that the copies are asynchronous and the call need not wait
+  // for them before it enqueues the stack
+  HIP_TRY(g->h_rows.acquire(sizeof(EmbedRow) * (size_t)M));
+  HIP_TRY(g->h_conds.acquire(sizeof(float) * (size_t)std::max(1, n_cond_all) * d));
+  memcpy(g->h_rows.p, rows.data(), sizeof(EmbedRow) * M);
+  HIP_TRY(hipMemcpyAsync(g->rows.p, g->h_rows.p, sizeof(EmbedRow) * M, hipMemcpyHostToDevice, g->stream));
   cbase = 0;
   for (int b = 0; b < B; b++) {
     const itts_code_prompt &p = ps[b];
-    if (p.n_cond > 0)
-      HIP_TRY(hipMemcpyAsync(g->conds.as<float>() + (size_t)cbase * d, p.conds, sizeof(float) * (size_t)p.n_cond * d,
+    if (p.n_cond > 0) {
+      float *hc = g->h_conds.as<float>() + (size_t)cbase * d;
+      memcpy(hc, p.conds, sizeof(float) * (size_t)p.n_cond * d);
+      HIP_TRY(hipMemcpyAsync(g->conds.as<float>() + (size_t)cbase * d, hc, sizeof(float) * (size_t)p.n_cond * d,
                              hipMemcpyHostToDevice, g->stream));
+    }
     HIP_TRY(launch_embed_rows(g->rows.as<EmbedRow>() + row0[b], T[b], g->conds.as<float>(), g->text_emb.as<float>(),
                               g->lang_emb.as<float>() + (size_t)p.lang_id * d, g->text_pos.as<float>(),
                               g->mel_emb.as<float>(), g->mel_pos.as<float>(), d,
                               g->px.as<float>() + (size_t)row0[b] * d, g->stream));
     cbase += p.n_cond;
   }
-  // the host arrays above are staged by the copies before they return
-  HIP_TRY(hipStreamSynchronize(g->stream));
+  HIP_TRY(g->h_rows.release(g->stream));
+  HIP_TRY(g->h_conds.release(g->stream));
   *M_out = M;
   return ITTS_OK;
 }
