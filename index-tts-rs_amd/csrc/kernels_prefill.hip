@@ -406,6 +406,30 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
   if constexpr (kFoldEarly) {
     if (fin && worker) fold_load(0, fv);
   }
+  // The epilogue's column constants on 64 x 64 tiles (one 32-column MFMA tile a wave): the
+  // bias (or the folded LayerNorm's c) and the folded G of the lane's column, loaded here so
+  // the epilogue does not start with a memory round trip.  Addresses selected, not loads
+  // predicated (a load behind a branch would make the compiler wait for the fold loads).
+  constexpr bool kColEarly = PROD && TM == 1 && TN == 1;
+  float cb = 0.0f, cg = 0.0f;
+  if constexpr (kColEarly) {
+    if (worker) {
+      const int n = min(n0 + wn * 32 + (lane & 31), N - 1);
+      cb = gload((kFoldIn && fin ? a.tfi.c : a.ql.bias) + n);
+      if constexpr (kFoldIn) cg = gload((fin ? a.tfi.G : a.ql.bias) + n);
+    }
+  }
+  // ... and the residual fold-out's gamma: worker thread t takes columns 16 (t & 3) .. +15
+  // of the tile (its item in the epilogue below), the same for every row
+  constexpr bool kGamEarly = kColEarly && EPI == kEpiResid;
+  float gam0[kGamEarly ? 16 : 1];
+  if constexpr (kGamEarly) {
+    if (worker && a.tfo.st) {
+      const float *gp = a.tfo.gamma + n0 + (tid & 3) * 16;
+#pragma unroll
+      for (int c = 0; c < 16; c++) gam0[c] = gload(gp + c);
+    }
+  }
   int i = 0;
   for (; i + 1 < ng; i += 2) {
     step(i, P0, P1);
@@ -551,9 +575,15 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       const bool live = worker && m0 + rl < M && n0 + c0 < N;
       float4 gam[VPT / 4];
       auto load_gamma = [&]() __attribute__((always_inline)) {
+        if constexpr (kGamEarly) {
+          static_assert(VPT == 16 && TPI == 4, "gamma loaded before the K loop for 16-column items");
 #pragma unroll
-        for (int c = 0; c < VPT / 4; c++)
-          gam[c] = live ? reinterpret_cast<const float4 *>(a.tfo.gamma + n0 + c0)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int c = 0; c < 4; c++) gam[c] = make_float4(gam0[4 * c], gam0[4 * c + 1], gam0[4 * c + 2], gam0[4 * c + 3]);
+        } else {
+#pragma unroll
+          for (int c = 0; c < VPT / 4; c++)
+            gam[c] = live ? reinterpret_cast<const float4 *>(a.tfo.gamma + n0 + c0)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       };
       if constexpr (TM == 1) load_gamma();
       __syncthreads();
@@ -564,7 +594,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
           for (int j = 0; j < TN; j++) {
             const int cl = wn * 32 * TN + j * 32 + (lane & 31), n = n0 + cl;
             if (n >= N) continue;
-            const float bias = a.ql.bias[n];
+            const float bias = kColEarly ? cb : a.ql.bias[n];
             const int rb = wm * 32 * TM + i2 * 32 + (lane >> 5) * 4;  // tile row of element 0
             // values first (straight-line), then the stores predicated on the row
             float outv[16];
@@ -647,8 +677,8 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       for (int j = 0; j < TN; j++) {
         const int cl = wn * 32 * TN + j * 32 + (lane & 31);
         const bool nl = n0 + cl < N;
-        const float bias = nl ? (fin ? a.tfi.c[n0 + cl] : a.ql.bias[n0 + cl]) : 0.0f;
-        const float gn = fin && nl ? a.tfi.G[n0 + cl] : 0.0f;
+        const float bias = kColEarly ? cb : nl ? (fin ? a.tfi.c[n0 + cl] : a.ql.bias[n0 + cl]) : 0.0f;
+        const float gn = kColEarly ? (fin ? cg : 0.0f) : fin && nl ? a.tfi.G[n0 + cl] : 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
@@ -697,8 +727,8 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
       for (int j = 0; j < TN; j++) {
         const int n = n0 + wn * 32 * TN + j * 32 + (lane & 31);
         if (n >= N) continue;
-        const float bias = fin ? a.tfi.c[n] : a.ql.bias[n];
-        const float gn = fin ? a.tfi.G[n] : 0.0f;
+        const float bias = kColEarly ? cb : fin ? a.tfi.c[n] : a.ql.bias[n];
+        const float gn = kColEarly ? (fin ? cg : 0.0f) : fin ? a.tfi.G[n] : 0.0f;
         const int rb = wm * 32 * TM + i2 * 32 + (lane >> 5) * 4;  // tile row of element 0
         // 128-row tiles: the sub-tile's 16 old values loaded together (registers for all 64
         // of the lane's would spill)
