@@ -185,6 +185,15 @@ __device__ inline float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+// The same function through 0.5 x (1 + tanh u) = x / (1 + exp(-2u)): one v_exp_f32 (2^t,
+// t = -2u log2 e) and one v_rcp_f32, each within about an ulp, instead of tanhf's
+// polynomial and branches; free of the cancellation in 1 + tanh u for negative x.  At
+// u -> -inf, 2^t -> inf and the result -> -0; at u -> +inf, -> x.
+__device__ inline float gelu_tanh_exp(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
+}
+
 // Sum over a block of NT threads; every thread receives the same value, formed in the
 // same order on every block (deterministic).
 template <int NT>

@@ -684,7 +684,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
           const int rl = wm * 32 * TM + i2 * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
           float v = acc[i2][j][e];
           if (fin) v = fold_row[rl].y * (v - fold_row[rl].x * gn);
-          T[rl * LDT + cl] = gelu_tanh(v + bias);
+          T[rl * LDT + cl] = gelu_tanh_exp(v + bias);
         }
       }
     __syncthreads();
@@ -1096,7 +1096,7 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
     for (int q = 0; q < kFewEPT; q++) {
       const int i = tid + 64 * kFewWaves * q, j = i >> 8, e = (i >> 6) & 3, ln = i & 63;
       const int m = 4 * (ln >> 5) + e, cl = 32 * j + (ln & 31), n = n0 + cl;
-      const float gv = gelu_tanh(FOLD ? row_rs[m] * (v[q] - row_mu[m] * ep_g[q]) + ep_b[q]
+      const float gv = gelu_tanh_exp(FOLD ? row_rs[m] * (v[q] - row_mu[m] * ep_g[q]) + ep_b[q]
                                       : v[q] + ep_b[q]);  // N is a multiple of 64 here
       gel[m][cl] = gv;
       if (m < M) {
