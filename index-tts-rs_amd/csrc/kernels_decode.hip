@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
       } else if constexpr (EPI == kEpiResid) {
         a.y[row] = a.y[row] + v;
       } else if constexpr (EPI == kEpiGelu) {
-        a.y[row] = gelu_tanh(v);
+        a.y[row] = gelu_tanh_exp(v);
       } else {
         const int d = a.qkv.d_model;
         const int pos = a.ctl != nullptr ? a.ctl->valid_len : a.qkv.pos0;

@@ -1067,7 +1067,7 @@ __device__ __forceinline__ void run(const PersistArgs &a, PersistShared &sh, flo
     if (loader) {
       const float mu = sh.red[24], rstd = sh.red[25];
       row_sums(m_fc, part, lw, lane,
-               [&](int r, float v) { out[r] = gelu_tanh(rstd * (v - mu * lp[bo_gf + r]) + lp[bo_cf + r]); });
+               [&](int r, float v) { out[r] = gelu_tanh_exp(rstd * (v - mu * lp[bo_gf + r]) + lp[bo_cf + r]); });
     }
     __syncthreads();
     if (pub) {
