@@ -451,13 +451,18 @@ __global__ void attn_combine_kernel(const float *part_o, const float *part_ml, i
 // MFMA units work on the current one: one barrier per K tile.  Rows of A may overlap (lda < K):
 // a kernel-size-k conv over rows d apart is one GEMM with K = k d and lda = d.
 // Requires K, lda, ldw % 4 == 0 and 16-byte aligned A and W.
-// (a, b) -> packed fp16 pairs hi = (ha, hb), lo = (la, lb) with a = ha + la, b = hb + lb
+// (a, b) -> packed fp16 pairs hi = (ha, hb), lo = (la, lb) with a = ha + la, b = hb + lb:
+// split_f16 on each value (hi clamped to the fp16 range, both rounded to nearest even),
+// the pair converted by one v_cvt_pk_f16_f32 per plane
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2e __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-  uint32_t h0, l0, h1, l1;
-  split_f16(a, h0, l0);
-  split_f16(b, h1, l1);
-  hi = h0 | (h1 << 16);
-  lo = l0 | (l1 << 16);
+  const f32x2e v = {a, b};
+  const f32x2e c = {__builtin_amdgcn_fmed3f(a, -65504.0f, 65504.0f), __builtin_amdgcn_fmed3f(b, -65504.0f, 65504.0f)};
+  const f16x2v h = __builtin_convertvector(c, f16x2v);
+  const f16x2v l = __builtin_convertvector(v - __builtin_convertvector(h, f32x2e), f16x2v);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
 }
 
 struct GemmLds {
@@ -474,28 +479,38 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   A += blockIdx.z * sa;
   W += blockIdx.z * sw;
   y += blockIdx.z * sy;
-  const int nk = (K + 63) / 64;
-  float4 ra[2], rw[2];
-  auto load = [&](int kt) {
+  // K tiles of 64, rounded up to a pair (a tile past K is split as zeros), so that the
+  // loop below runs whole pairs with no conditional step or store
+  const int nk = (K + 127) / 128 * 2;
+  // Two K tiles of fp32 loads in flight, in two register sets: a tile's loads are issued
+  // two tiles before its split into LDS, so each waits behind a tile of MFMA work and a
+  // barrier rather than being the next thing waited for (one set: each K tile cost about
+  // one load latency).  The loads are unpredicated, with the row and k indexes clamped
+  // into the operands (so that the compiler's wait counting keeps the later set in
+  // flight).  Rows past M or N are loaded as a copy of the last row: they reach only output
+  // rows and columns that are not stored.  Values past K are zeroed in W's planes (A's
+  // clamped values there are finite, so the products vanish).
+  float4 ra[2][2], rw[2][2];
+  auto load = [&](int kt, float4(&a4)[2], float4(&w4)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-      const int idx = tid + 512 * j, row = idx >> 4, k = kt * 64 + (idx & 15) * 4;
-      ra[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      rw[j] = ra[j];
-      if (m0 + row < M && k < K) ra[j] = *reinterpret_cast<const float4 *>(A + (size_t)(m0 + row) * lda + k);
-      if (n0 + row < N && k < K) rw[j] = *reinterpret_cast<const float4 *>(W + (size_t)(n0 + row) * ldw + k);
+      const int idx = tid + 512 * j, row = idx >> 4, k = min(kt * 64 + (idx & 15) * 4, K - 4);
+      a4[j] = *reinterpret_cast<const float4 *>(A + (size_t)min(m0 + row, M - 1) * lda + k);
+      w4[j] = *reinterpret_cast<const float4 *>(W + (size_t)min(n0 + row, N - 1) * ldw + k);
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](int buf, int kt, const float4(&a4)[2], const float4(&w4)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int idx = tid + 512 * j, row = idx >> 4, c4 = idx & 15;
       const int off = swz(row, c4 >> 1) + (c4 & 1) * 4;
+      const bool kin = kt * 64 + c4 * 4 < K;
+      const float4 av = a4[j], wv4 = kin ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
       uint32_t ah0, al0, ah1, al1, wh0, wl0, wh1, wl1;
-      split2(ra[j].x, ra[j].y, ah0, al0);
-      split2(ra[j].z, ra[j].w, ah1, al1);
-      split2(rw[j].x, rw[j].y, wh0, wl0);
-      split2(rw[j].z, rw[j].w, wh1, wl1);
+      split2(av.x, av.y, ah0, al0);
+      split2(av.z, av.w, ah1, al1);
+      split2(wv4.x, wv4.y, wh0, wl0);
+      split2(wv4.z, wv4.w, wh1, wl1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][0][off]) = make_uint2(ah0, ah1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][1][off]) = make_uint2(al0, al1);
       *reinterpret_cast<uint2 *>(&sh.w[buf][0][off]) = make_uint2(wh0, wh1);
@@ -505,12 +520,13 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
+  // K tile kt: LDS buffer kt & 1; its registers set kt & 1, reloaded with tile kt + 2 once
+  // the tile is in LDS.  Tiles past the end are loaded clamped; the last step's store
+  // (tile nk, all zeros) goes to the buffer no later step reads.
+  auto tile = [&](int kt, float4(&a_cur)[2], float4(&w_cur)[2], const float4(&a_nxt)[2],
+                  const float4(&w_nxt)[2]) __attribute__((always_inline)) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) load(kt + 1);
+    load(min(kt + 2, nk - 1), a_cur, w_cur);
 #pragma unroll
     for (int k2 = 0; k2 < 2; k2++) {
       const int kk = kg * 2 + k2;
@@ -524,8 +540,16 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
       acc = MFMA16(ah, bl, acc, 0, 0, 0);
       acc = MFMA16(al, bh, acc, 0, 0, 0);
     }
-    if (kt + 1 < nk) store(buf ^ 1);
+    store(buf ^ 1, kt + 1, a_nxt, w_nxt);
     __syncthreads();
+  };
+  load(0, ra[0], rw[0]);
+  load(min(1, nk - 1), ra[1], rw[1]);
+  store(0, 0, ra[0], rw[0]);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    tile(kt, ra[0], rw[0], ra[1], rw[1]);
+    tile(kt + 1, ra[1], rw[1], ra[0], rw[0]);
   }
   // the second K half's sums to LDS (the loop ended on a barrier), added by the first
   float *red = reinterpret_cast<float *>(&sh.a[0][0][0]) + wv * 1024 + lane;
