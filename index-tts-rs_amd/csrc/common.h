@@ -113,6 +113,20 @@ __device__ inline void split_f16(float x, uint32_t &hi, uint32_t &lo) {
   lo = __builtin_bit_cast(uint16_t, l);
 }
 
+// split_f16 of a pair (a, b), packed: hi = (hi_a, hi_b), lo = (lo_a, lo_b), low half first.
+// The same values as two split_f16 calls (both conversions round to nearest even), formed
+// by one v_cvt_pk_f16_f32 per plane and a single v_med3_f32 clamp per value.
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2e __attribute__((ext_vector_type(2)));
+__device__ inline void split_f16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  const f32x2e v = {a, b};
+  const f32x2e c = {__builtin_amdgcn_fmed3f(a, -65504.0f, 65504.0f), __builtin_amdgcn_fmed3f(b, -65504.0f, 65504.0f)};
+  const f16x2v h = __builtin_convertvector(c, f16x2v);
+  const f16x2v l = __builtin_convertvector(v - __builtin_convertvector(h, f32x2e), f16x2v);
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
 // (scale, bias) of one (row, group).
 template <int PT>
 __device__ inline float2 load_param(const void *params, size_t idx) {

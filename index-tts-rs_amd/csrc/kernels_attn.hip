@@ -55,11 +55,10 @@ __device__ __forceinline__ void load8(const void *base, size_t idx, float v[8]) 
 __device__ __forceinline__ void split8(const float v[8], u32x4 &hi, u32x4 &lo) {
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    uint32_t h0, l0, h1, l1;
-    split_f16(v[2 * j], h0, l0);
-    split_f16(v[2 * j + 1], h1, l1);
-    hi[j] = h0 | (h1 << 16);
-    lo[j] = l0 | (l1 << 16);
+    uint32_t h, l;
+    split_f16x2(v[2 * j], v[2 * j + 1], h, l);
+    hi[j] = h;
+    lo[j] = l;
   }
 }
 
@@ -220,12 +219,11 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
   #pragma unroll
           for (int j = 0; j < 8; j++) {
             const int e = e0 + j;
-            uint32_t ha, la, hb2, lb;
-            split_f16(a[j], ha, la);
-            split_f16(b[j], hb2, lb);
+            uint32_t hab, lab;
+            split_f16x2(a[j], b[j], hab, lab);
             const int idx = e * 64 + ((((2 * kp) >> 3) ^ ((e >> 1) & 7)) << 3) + ((2 * kp) & 7);
-            *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = ha | (hb2 << 16);
-            *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = la | (lb << 16);
+            *reinterpret_cast<uint32_t *>(&sh.vt[0][idx]) = hab;
+            *reinterpret_cast<uint32_t *>(&sh.vt[1][idx]) = lab;
           }
         }
       }
@@ -267,17 +265,20 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
       const float mn = fmaxf(m[i], tmax[i]);
       const float corr = m[i] == -INFINITY ? 1.0f : __expf(m[i] - mn);
       const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-      float psum = 0.0f;
+      float psum = 0.0f, p[2];
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        const float p = s[kt] == -INFINITY ? 0.0f : __expf(s[kt] - mn);
-        psum += p;
-        uint32_t ph, pl;
-        split_f16(p, ph, pl);
+        p[kt] = s[kt] == -INFINITY ? 0.0f : __expf(s[kt] - mn);
+        psum += p[kt];
+      }
+      uint32_t ph, pl;  // the two keys' (hi, lo) pairs, key tile 0 in the low halves
+      split_f16x2(p[0], p[1], ph, pl);
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
         const int key = kt * 32 + (lane & 31);
         const int o = r * 64 + (((key >> 3) ^ ((r >> 1) & 7)) << 3) + (key & 7);
-        pw[o] = (uint16_t)ph;
-        pw[32 * kFK + o] = (uint16_t)pl;
+        pw[o] = (uint16_t)(ph >> (16 * kt));
+        pw[32 * kFK + o] = (uint16_t)(pl >> (16 * kt));
       }
       l[i] = l[i] * corr + psum;
       O[0][i] *= corr;
@@ -313,12 +314,11 @@ __global__ __launch_bounds__(128) void attn_flash_kernel(const float *q, int d, 
     if (t < T) {
       const size_t row = (size_t)t * d + h * 64 + (lane & 31);
       uint32_t hi, lo;
-      split_f16(v0, hi, lo);
+      split_f16x2(v0, v1, hi, lo);
       out.hi[row] = (uint16_t)hi;
       out.lo[row] = (uint16_t)lo;
-      split_f16(v1, hi, lo);
-      out.hi[row + 32] = (uint16_t)hi;
-      out.lo[row + 32] = (uint16_t)lo;
+      out.hi[row + 32] = (uint16_t)(hi >> 16);
+      out.lo[row + 32] = (uint16_t)(lo >> 16);
       if ((lane & 31) == 0) out.gs[(size_t)t * (d / 64) + h] = gsum;
     }
   }

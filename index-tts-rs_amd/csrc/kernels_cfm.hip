@@ -167,11 +167,10 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chu
 __device__ __forceinline__ void split8(const float v[8], u32x4v &hi, u32x4v &lo) {
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    uint32_t h0, l0, h1, l1;
-    split_f16(v[2 * j], h0, l0);
-    split_f16(v[2 * j + 1], h1, l1);
-    hi[j] = h0 | (h1 << 16);
-    lo[j] = l0 | (l1 << 16);
+    uint32_t h, l;
+    split_f16x2(v[2 * j], v[2 * j + 1], h, l);
+    hi[j] = h;
+    lo[j] = l;
   }
 }
 
@@ -451,19 +450,6 @@ __global__ void attn_combine_kernel(const float *part_o, const float *part_ml, i
 // MFMA units work on the current one: one barrier per K tile.  Rows of A may overlap (lda < K):
 // a kernel-size-k conv over rows d apart is one GEMM with K = k d and lda = d.
 // Requires K, lda, ldw % 4 == 0 and 16-byte aligned A and W.
-// (a, b) -> packed fp16 pairs hi = (ha, hb), lo = (la, lb) with a = ha + la, b = hb + lb:
-// split_f16 on each value (hi clamped to the fp16 range, both rounded to nearest even),
-// the pair converted by one v_cvt_pk_f16_f32 per plane
-typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
-typedef float f32x2e __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-  const f32x2e v = {a, b};
-  const f32x2e c = {__builtin_amdgcn_fmed3f(a, -65504.0f, 65504.0f), __builtin_amdgcn_fmed3f(b, -65504.0f, 65504.0f)};
-  const f16x2v h = __builtin_convertvector(c, f16x2v);
-  const f16x2v l = __builtin_convertvector(v - __builtin_convertvector(h, f32x2e), f16x2v);
-  hi = __builtin_bit_cast(uint32_t, h);
-  lo = __builtin_bit_cast(uint32_t, l);
-}
 
 struct GemmLds {
   uint16_t a[2][2][64 * 64];  // [buffer][plane][row][k]
@@ -507,10 +493,10 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
       const bool kin = kt * 64 + c4 * 4 < K;
       const float4 av = a4[j], wv4 = kin ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
       uint32_t ah0, al0, ah1, al1, wh0, wl0, wh1, wl1;
-      split2(av.x, av.y, ah0, al0);
-      split2(av.z, av.w, ah1, al1);
-      split2(wv4.x, wv4.y, wh0, wl0);
-      split2(wv4.z, wv4.w, wh1, wl1);
+      split_f16x2(av.x, av.y, ah0, al0);
+      split_f16x2(av.z, av.w, ah1, al1);
+      split_f16x2(wv4.x, wv4.y, wh0, wl0);
+      split_f16x2(wv4.z, wv4.w, wh1, wl1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][0][off]) = make_uint2(ah0, ah1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][1][off]) = make_uint2(al0, al1);
       *reinterpret_cast<uint2 *>(&sh.w[buf][0][off]) = make_uint2(wh0, wh1);

@@ -801,13 +801,11 @@ __global__ __launch_bounds__(256) void ln_rows_wave_kernel(const float *x, const
 #pragma unroll
   for (int j = 0; j < NV; j++) {
     const size_t i = (size_t)row * d + 256 * j + 4 * lane;
-    uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-    split_f16(v[j].x, h0, l0);
-    split_f16(v[j].y, h1, l1);
-    split_f16(v[j].z, h2, l2);
-    split_f16(v[j].w, h3, l3);
-    *reinterpret_cast<uint2 *>(y.hi + i) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
-    *reinterpret_cast<uint2 *>(y.lo + i) = make_uint2(l0 | (l1 << 16), l2 | (l3 << 16));
+    uint32_t h01, l01, h23, l23;
+    split_f16x2(v[j].x, v[j].y, h01, l01);
+    split_f16x2(v[j].z, v[j].w, h23, l23);
+    *reinterpret_cast<uint2 *>(y.hi + i) = make_uint2(h01, h23);
+    *reinterpret_cast<uint2 *>(y.lo + i) = make_uint2(l01, l23);
     // group 4 j + lane / 16: the 16 lanes of this DPP row
     float g = (v[j].x + v[j].y) + (v[j].z + v[j].w);
     g += dpp_pair<0xB1>(g);

@@ -641,11 +641,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
             const float g1 = ((e & 2) ? gq.w : gq.y) * v1;
             gsum += g0;
             gsum += g1;
-            uint32_t h0, l0, h1, l1;
-            split_f16(g0, h0, l0);
-            split_f16(g1, h1, l1);
-            hw[e >> 1] = h0 | (h1 << 16);
-            lw[e >> 1] = l0 | (l1 << 16);
+            split_f16x2(g0, g1, hw[e >> 1], lw[e >> 1]);
           }
           if (live) {
             gstore(reinterpret_cast<uint4 *>(a.tfo.o.hi + (size_t)m * N + n + c), make_uint4(hw[0], hw[1], hw[2], hw[3]));
@@ -705,11 +701,7 @@ __global__ __launch_bounds__(PROD ? 512 : 256, (PROD && TM == 1) ? 4 : 1) void g
           const float v0 = T[rl * LDT + c0 + c + e], v1 = T[rl * LDT + c0 + c + e + 1];
           sum += v0;
           sum += v1;
-          uint32_t h0, l0, h1, l1;
-          split_f16(v0, h0, l0);
-          split_f16(v1, h1, l1);
-          hw[e >> 1] = h0 | (h1 << 16);
-          lw[e >> 1] = l0 | (l1 << 16);
+          split_f16x2(v0, v1, hw[e >> 1], lw[e >> 1]);
         }
         if (live) {
           gstore(reinterpret_cast<uint4 *>(a.xo.hi + (size_t)m * N + n + c), make_uint4(hw[0], hw[1], hw[2], hw[3]));
@@ -948,11 +940,7 @@ __global__ __launch_bounds__(64 * kFewWaves) void few_kernel(GemmArgs a, int nN,
 #pragma unroll
             for (int e2 = 0; e2 < 2; e2++) {
               gsum += y[2 * e2] + y[2 * e2 + 1];
-              uint32_t h0, l0, h1, l1;
-              split_f16(y[2 * e2], h0, l0);
-              split_f16(y[2 * e2 + 1], h1, l1);
-              hw[2 * q2 + e2] = h0 | (h1 << 16);
-              lw[2 * q2 + e2] = l0 | (l1 << 16);
+              split_f16x2(y[2 * e2], y[2 * e2 + 1], hw[2 * q2 + e2], lw[2 * q2 + e2]);
             }
           }
           xa[0][0][kp][sub] = u32x4{hw[0], hw[1], hw[2], hw[3]};
