@@ -16,6 +16,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/itts_hip.h"
@@ -70,16 +71,8 @@ struct Buf {
   }
 };
 
-// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart) on the estimator's
-// stream: row blocks of 64 and more on the split-fp16 MFMA GEMM, fewer rows (the per-batch
-// timestep, AdaLN and WaveNet-conditioning projections, forwards of under 64 frames) and
-// operands the MFMA GEMM cannot take on the few-row fp32 product.
-hipError_t gemm(hipStream_t st, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                int ldy, float beta) {
-  if (M >= 64 && itts::cfm_gemm_fits(A, lda, W, ldw, K))
-    return itts::cfm_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st);
-  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, st);
-}
+hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
+                int ldy, float beta);
 
 struct Block {
   const float *wqkv, *wo, *w13, *w2, *skip_w, *skip_b, *an_w, *fn_w;
@@ -110,7 +103,11 @@ struct itts_cfm {
   Buf x, xt, merged, catc, refm, sty, io_a, io_b;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   float last_ms = -1.0f;
+  // the weights' fp16 hi/lo quads for the MFMA GEMM, split on first use: (W, ldw, N, K) ->
+  // cfm_split_weights output
+  std::map<std::tuple<const float *, int, int, int>, uint4 *> wsplit;
   ~itts_cfm() {
+    for (auto &kv : wsplit) (void)hipFree(kv.second);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (arena) (void)hipFree(arena);
@@ -119,6 +116,37 @@ struct itts_cfm {
 };
 
 namespace {
+
+// The split quads of the weight view (W, ldw, N, K), made on the estimator's stream at its
+// first use (the weights are constant while the estimator lives); nullptr on failure.
+uint4 *split_weights(itts_cfm *m, const float *W, int ldw, int N, int K) {
+  const auto key = std::make_tuple(W, ldw, N, K);
+  auto it = m->wsplit.find(key);
+  if (it != m->wsplit.end()) return it->second;
+  uint4 *p = nullptr;
+  if (hipMalloc(&p, itts::cfm_split_weights_quads(N, K) * sizeof(uint4)) != hipSuccess) return nullptr;
+  if (itts::cfm_split_weights(W, ldw, N, K, p, m->s) != hipSuccess) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  m->wsplit.emplace(key, p);
+  return p;
+}
+
+// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart) on the estimator's
+// stream: row blocks of 64 and more on the split-fp16 MFMA GEMM over the weight's split
+// quads, fewer rows (the per-batch timestep, AdaLN and WaveNet-conditioning projections,
+// forwards of under 64 frames) and operands the MFMA GEMM cannot take on the few-row fp32
+// product.
+hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
+                int ldy, float beta) {
+  if (M >= 64 && itts::cfm_gemm_fits(A, lda, W, ldw, K)) {
+    const uint4 *wp = split_weights(m, W, ldw, N, K);
+    if (!wp) return hipErrorOutOfMemory;
+    return itts::cfm_gemm_split_w(1, M, N, K, A, lda, 0, wp, y, ldy, 0, beta, m->s);
+  }
+  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, m->s);
+}
 
 itts_status check_config(const itts_cfm_config &c) {
   if (c.n_heads < 1 || c.dim != 64 * c.n_heads || c.n_layers < 1 || c.inter < 1 || c.in_ch < 1 || c.style_dim < 0 ||
@@ -174,10 +202,10 @@ itts_status timestep(itts_cfm *m, int e, int B, float *out) {
   hipStream_t s = m->s;
   CK(cfm_temb(m->tdev.p, B, m->emb.p, s));
   CK(cfm_bias_rows(m->th.p, d, m->te_b0[e], B, d, s));
-  CK(gemm(m->s, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 1.0f));
+  CK(gemm(m, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 1.0f));
   CK(cfm_silu(m->th.p, m->th.p, B * d, s));
   CK(cfm_bias_rows(out, d, m->te_b2[e], B, d, s));
-  CK(gemm(m->s, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 1.0f));
+  CK(gemm(m, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 1.0f));
   return ITTS_OK;
 }
 
@@ -194,16 +222,16 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
   if (itts_status st = timestep(m, 0, B, m->t1.p)) return st;
   if (itts_status st = timestep(m, 1, B, m->t2.p)) return st;
   CK(cfm_bias_rows(m->mods.p, na2, m->ada_b, B, na2, s));
-  CK(gemm(s, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 1.0f));
+  CK(gemm(m, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 1.0f));
   CK(cfm_bias_rows(m->wng.p, 2 * d * NL, m->wc_b, B, 2 * d * NL, s));
-  CK(gemm(s, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 1.0f));
+  CK(gemm(m, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 1.0f));
   CK(cfm_silu(m->t1.p, m->st.p, B * d, s));
   CK(cfm_bias_rows(m->fmod.p, 2 * d, m->fa_b, B, 2 * d, s));
-  CK(gemm(s, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 1.0f));
+  CK(gemm(m, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 1.0f));
   // h = cond_x_merge_linear(x_merged)
   float *cur = m->hA.p, *oth = m->hB.p;
   CK(cfm_bias_rows(cur, d, m->merge_b, R, d, s));
-  CK(gemm(s, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 1.0f));
+  CK(gemm(m, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 1.0f));
   // U-ViT blocks with long skips (cfm.rs:553-563)
   int nsk = 0;
   for (int i = 0; i < Lc; i++) {
@@ -212,31 +240,31 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     if (i > split && nsk > 0) {  // skip_in_linear([h, skip]) as two accumulating GEMMs
       const float *sk = m->skips[--nsk].p;
       CK(cfm_bias_rows(oth, d, b.skip_b, R, d, s));
-      CK(gemm(s, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 1.0f));
-      CK(gemm(s, R, d, d, sk, d, b.skip_w + d, 2 * d, oth, d, 1.0f));
+      CK(gemm(m, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 1.0f));
+      CK(gemm(m, R, d, d, sk, d, b.skip_w + d, 2 * d, oth, d, 1.0f));
       xin = oth;
       oth = cur;
       cur = xin;
     }
     const float *mod_a = m->mods.p + (size_t)(2 * i) * 2 * d, *mod_f = m->mods.p + (size_t)(2 * i + 1) * 2 * d;
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_a, na2, b.an_w, s));
-    CK(gemm(s, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
+    CK(gemm(m, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
     CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p,
                      reinterpret_cast<uint16_t *>(m->kvs.p), m->n_cu, s));
-    CK(gemm(s, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
+    CK(gemm(m, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
-    CK(gemm(s, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
+    CK(gemm(m, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
     CK(cfm_swiglu(m->gu.p, R, F, m->act.p, s));
-    CK(gemm(s, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
+    CK(gemm(m, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
     if (i < split) CK(hipMemcpyAsync(m->skips[nsk++].p, xin, sizeof(float) * R * d, hipMemcpyDeviceToDevice, s));
   }
   // transformer.norm, x_res = skip_linear([h, x_t]), h = conv1(x_res)
   CK(cfm_adaln(cur, m->n.p, R, T, d, m->mods.p + (size_t)(2 * Lc) * 2 * d, na2, m->tn_w, s));
   CK(cfm_bias_rows(m->xres.p, d, m->skl_b, R, d, s));
-  CK(gemm(s, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 1.0f));
-  CK(gemm(s, R, d, C, x_t, C, m->skl_w + d, d + C, m->xres.p, d, 1.0f));
+  CK(gemm(m, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 1.0f));
+  CK(gemm(m, R, d, C, x_t, C, m->skl_w + d, d + C, m->xres.p, d, 1.0f));
   CK(cfm_bias_rows(oth, d, m->c1_b, R, d, s));
-  CK(gemm(s, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 1.0f));
+  CK(gemm(m, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 1.0f));
   // WaveNet (cfm.rs:373-408): h in a zero-padded [B][T + 2 pad][d] buffer
   CK(cfm_pad_rows(oth, B, T, d, pad, m->hpad.p, s));
   CK(hipMemsetAsync(m->oacc.p, 0, sizeof(float) * R * d, s));
@@ -247,19 +275,21 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     const int rso = last ? d : 2 * d;
     // all taps as one product: row t of the padded input read K * d wide (rows t .. t+K-1);
     // d is a multiple of 64, so the operands always suit the MFMA GEMM
-    CK(cfm_gemm(B, T, 2 * d, K * d, m->hpad.p, d, sp, w.in_w, K * d, 0, m->acts.p, 2 * d, (long)T * 2 * d, 0.0f, s));
+    const uint4 *in_q = split_weights(m, w.in_w, K * d, 2 * d, K * d);
+    if (!in_q) return cerr(ITTS_E_DEVICE, "out of device memory for the split WaveNet weights");
+    CK(cfm_gemm_split_w(B, T, 2 * d, K * d, m->hpad.p, d, sp, in_q, m->acts.p, 2 * d, (long)T * 2 * d, 0.0f, s));
     CK(cfm_gate(m->acts.p, w.in_b, m->wng.p + (size_t)l * 2 * d, 2 * d * NL, R, T, d, m->act.p, s));
-    CK(gemm(s, R, rso, d, m->act.p, d, w.rs_w, d, m->rs.p, rso, 0.0f));
+    CK(gemm(m, R, rso, d, m->act.p, d, w.rs_w, d, m->rs.p, rso, 0.0f));
     CK(cfm_res_skip(m->rs.p, w.rs_b, last ? 1 : 0, R, T, d, pad, m->hpad.p, m->oacc.p, s));
   }
   // h = wavenet + res_projection(x_res); FinalLayer; conv2
   CK(cfm_add_bias(m->oacc.p, d, m->rp_b, R, d, s));
-  CK(gemm(s, R, d, d, m->xres.p, d, m->rp_w, d, m->oacc.p, d, 1.0f));
+  CK(gemm(m, R, d, d, m->xres.p, d, m->rp_w, d, m->oacc.p, d, 1.0f));
   CK(cfm_final_norm(m->oacc.p, m->n.p, R, T, d, m->fmod.p, s));
   CK(cfm_bias_rows(cur, d, m->fl_b, R, d, s));
-  CK(gemm(s, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 1.0f));
+  CK(gemm(m, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 1.0f));
   CK(cfm_bias_rows(m->v.p, C, m->c2_b, R, C, s));
-  CK(gemm(s, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 1.0f));
+  CK(gemm(m, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 1.0f));
   return ITTS_OK;
 }
 
@@ -473,7 +503,7 @@ itts_status itts_cfm_solve_euler(itts_cfm *m, const float *cat_condition, int32_
   CK(hipMemsetAsync(m->merged.p, 0, sizeof(float) * 2 * T * MD, s));
   CK(cfm_static_tail(m->merged.p, MD, C, d, S, T, m->refm.p, T_ref, m->sty.p, s));
   CK(cfm_bias_rows(m->merged.p + 2 * C, MD, m->cond_b, 2 * T, d, s));
-  CK(gemm(m->s, T, d, d, m->catc.p, d, m->cond_w, d, m->merged.p + 2 * C, MD, 1.0f));
+  CK(gemm(m, T, d, d, m->catc.p, d, m->cond_w, d, m->merged.p + 2 * C, MD, 1.0f));
   CK(hipEventRecord(m->e0, s));
   const float dt = 1.0f / (float)n_timesteps;
   for (int step = 0; step < n_timesteps; step++) {

@@ -306,6 +306,13 @@ int cfm_kv_split_halves(int B, int T, int H);
 bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K);
 hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
                     float *y, int ldy, long sy, float beta, hipStream_t s);
+// The constant operand W split once into fp16 hi/lo quads (cfm_split_weights_quads(N, K)
+// uint4 at out, rows padded to 64 and k to 128 with zeros), and the product over them:
+// the same values as cfm_gemm on W (K, lda multiples of 4, A 16-byte aligned).
+size_t cfm_split_weights_quads(int N, int K);
+hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s);
+hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
+                            float *y, int ldy, long sy, float beta, hipStream_t s);
 // The same product in fp32 FMAs for few rows (any M, any alignment; float4 loads when K,
 // lda, ldw, sa, sw are multiples of 4 and A, W are 16-byte aligned); beta 0 never reads y.
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,

@@ -456,9 +456,27 @@ struct GemmLds {
   uint16_t w[2][2][64 * 64];
 };
 
+// W [N][ldw] (k < K) -> the pre-split quads split_gemm_kernel<true> reads, zeros past N and K
+__global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int kp4, long n, uint4 *out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int r = (int)(i / kp4), k = (int)(i % kp4) * 4;
+  uint4 q = make_uint4(0u, 0u, 0u, 0u);
+  if (r < N && k < K) {
+    const float4 v = *reinterpret_cast<const float4 *>(W + (size_t)r * ldw + k);
+    split_f16x2(v.x, v.y, q.x, q.z);
+    split_f16x2(v.z, v.w, q.y, q.w);
+  }
+  out[i] = q;
+}
+
+// PRE: W comes split already (cfm_split_weights): per row, 16 bytes per 4 values of k, {hi
+// (k, k+1), hi (k+2, k+3), lo (k, k+1), lo (k+2, k+3)}, wkp4 quads a row, rows padded to a
+// multiple of 64 and k to a multiple of 128 with zeros, copied to LDS as they are.
+template <bool PRE>
 __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const float *W, int ldw,
-                                                         long sw, float *y, int ldy, long sy, int M, int N, int K,
-                                                         float beta) {
+                                                         long sw, const uint4 *Wp, int wkp4, float *y, int ldy,
+                                                         long sy, int M, int N, int K, float beta) {
   __shared__ GemmLds sh;
   const int tid = threadIdx.x, lane = tid & 63, wv = (tid >> 6) & 3, kg = tid >> 8, wm = wv >> 1, wn = wv & 1;
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
@@ -482,7 +500,11 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
     for (int j = 0; j < 2; j++) {
       const int idx = tid + 512 * j, row = idx >> 4, k = min(kt * 64 + (idx & 15) * 4, K - 4);
       a4[j] = *reinterpret_cast<const float4 *>(A + (size_t)min(m0 + row, M - 1) * lda + k);
-      w4[j] = *reinterpret_cast<const float4 *>(W + (size_t)min(n0 + row, N - 1) * ldw + k);
+      if constexpr (PRE) {
+        w4[j] = __builtin_bit_cast(float4, Wp[(size_t)(n0 + row) * wkp4 + kt * 16 + (idx & 15)]);
+      } else {
+        w4[j] = *reinterpret_cast<const float4 *>(W + (size_t)min(n0 + row, N - 1) * ldw + k);
+      }
     }
   };
   auto store = [&](int buf, int kt, const float4(&a4)[2], const float4(&w4)[2]) __attribute__((always_inline)) {
@@ -491,12 +513,18 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
       const int idx = tid + 512 * j, row = idx >> 4, c4 = idx & 15;
       const int off = swz(row, c4 >> 1) + (c4 & 1) * 4;
       const bool kin = kt * 64 + c4 * 4 < K;
-      const float4 av = a4[j], wv4 = kin ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 av = a4[j];
       uint32_t ah0, al0, ah1, al1, wh0, wl0, wh1, wl1;
       split_f16x2(av.x, av.y, ah0, al0);
       split_f16x2(av.z, av.w, ah1, al1);
-      split_f16x2(wv4.x, wv4.y, wh0, wl0);
-      split_f16x2(wv4.z, wv4.w, wh1, wl1);
+      if constexpr (PRE) {
+        const uint4 q = __builtin_bit_cast(uint4, w4[j]);
+        wh0 = q.x, wh1 = q.y, wl0 = q.z, wl1 = q.w;
+      } else {
+        const float4 wv4 = kin ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        split_f16x2(wv4.x, wv4.y, wh0, wl0);
+        split_f16x2(wv4.z, wv4.w, wh1, wl1);
+      }
       *reinterpret_cast<uint2 *>(&sh.a[buf][0][off]) = make_uint2(ah0, ah1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][1][off]) = make_uint2(al0, al1);
       *reinterpret_cast<uint2 *>(&sh.w[buf][0][off]) = make_uint2(wh0, wh1);
@@ -808,8 +836,24 @@ bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K) {
 hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
                     float *y, int ldy, long sy, float beta, hipStream_t s) {
   if (batch < 1 || M < 1 || N < 1 || K < 1 || !cfm_gemm_fits(A, lda, W, ldw, K)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_gemm_kernel, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa, W,
-                     ldw, sw, y, ldy, sy, M, N, K, beta);
+  hipLaunchKernelGGL(split_gemm_kernel<false>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
+                     W, ldw, sw, nullptr, 0, y, ldy, sy, M, N, K, beta);
+  return hipGetLastError();
+}
+size_t cfm_split_weights_quads(int N, int K) { return (size_t)((N + 63) / 64 * 64) * ((K + 127) / 128 * 32); }
+hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s) {
+  if (N < 1 || K < 4 || K % 4 || ldw % 4 || ldw < K || (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
+  const int kp4 = (K + 127) / 128 * 32;
+  const long n = (long)((N + 63) / 64 * 64) * kp4;
+  hipLaunchKernelGGL(split_weights_kernel, dim3(nblk(n)), dim3(256), 0, s, W, ldw, N, K, kp4, n, out);
+  return hipGetLastError();
+}
+hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
+                            float *y, int ldy, long sy, float beta, hipStream_t s) {
+  if (batch < 1 || M < 1 || N < 1 || K < 4 || K % 4 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || !Wp)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(split_gemm_kernel<true>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
+                     nullptr, 0, 0, Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta);
   return hipGetLastError();
 }
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
