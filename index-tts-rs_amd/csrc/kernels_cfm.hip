@@ -344,12 +344,14 @@ __global__ __launch_bounds__(128) void cfm_attn_kernel(const float *qkv, const f
     for (int i = 0; i < 16; i++) {
       const float s[2] = {S[0][i], S[1][i]};
       const float mn = fmaxf(m[i], tmax[i]);
-      const float corr = m[i] == -INFINITY ? 1.0f : expf(m[i] - mn);
+      // (__expf: v_exp_f32 on a pre-scaled argument, within a few ulp; the scores' own
+      // rounding is far larger)
+      const float corr = m[i] == -INFINITY ? 1.0f : __expf(m[i] - mn);
       const int r = (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
       float psum = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        const float p = s[kt] == -INFINITY ? 0.0f : expf(s[kt] - mn);
+        const float p = s[kt] == -INFINITY ? 0.0f : __expf(s[kt] - mn);
         psum += p;
         uint32_t ph, pl;
         split_f16(p, ph, pl);
