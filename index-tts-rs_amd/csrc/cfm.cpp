@@ -103,9 +103,9 @@ struct itts_cfm {
   Buf x, xt, merged, catc, refm, sty, io_a, io_b;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   float last_ms = -1.0f;
-  // the weights' fp16 hi/lo quads for the MFMA GEMM, split on first use: (W, ldw, N, K) ->
-  // cfm_split_weights output
-  std::map<std::tuple<const float *, int, int, int>, uint4 *> wsplit;
+  // the weights' fp16 hi/lo quads for the MFMA GEMM, split on first use: (W, ldw, N, K,
+  // interleave) -> cfm_split_weights output
+  std::map<std::tuple<const float *, int, int, int, int>, uint4 *> wsplit;
   ~itts_cfm() {
     for (auto &kv : wsplit) (void)hipFree(kv.second);
     if (e0) (void)hipEventDestroy(e0);
@@ -117,15 +117,16 @@ struct itts_cfm {
 
 namespace {
 
-// The split quads of the weight view (W, ldw, N, K), made on the estimator's stream at its
-// first use (the weights are constant while the estimator lives); nullptr on failure.
-uint4 *split_weights(itts_cfm *m, const float *W, int ldw, int N, int K) {
-  const auto key = std::make_tuple(W, ldw, N, K);
+// The split quads of the weight view (W, ldw, N, K; rows interleaved when ilv > 0), made on
+// the estimator's stream at its first use (the weights are constant while the estimator
+// lives); nullptr on failure.
+uint4 *split_weights(itts_cfm *m, const float *W, int ldw, int N, int K, int ilv = 0) {
+  const auto key = std::make_tuple(W, ldw, N, K, ilv);
   auto it = m->wsplit.find(key);
   if (it != m->wsplit.end()) return it->second;
   uint4 *p = nullptr;
   if (hipMalloc(&p, itts::cfm_split_weights_quads(N, K) * sizeof(uint4)) != hipSuccess) return nullptr;
-  if (itts::cfm_split_weights(W, ldw, N, K, p, m->s) != hipSuccess) {
+  if (itts::cfm_split_weights(W, ldw, N, K, p, m->s, ilv) != hipSuccess) {
     (void)hipFree(p);
     return nullptr;
   }
@@ -253,8 +254,15 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
                      reinterpret_cast<uint16_t *>(m->kvs.p), m->n_cu, s));
     CK(gemm(m, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
-    CK(gemm(m, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
-    CK(cfm_swiglu(m->gu.p, R, F, m->act.p, s));
+    if (R >= 64 && F % 32 == 0 && cfm_gemm_fits(m->n.p, d, b.w13, d, d)) {
+      // the SwiGLU in the [w1; w3] product's epilogue, over rows interleaved per 32
+      const uint4 *q13 = split_weights(m, b.w13, d, 2 * F, d, F);
+      if (!q13) return cerr(ITTS_E_DEVICE, "out of device memory for the split FFN weights");
+      CK(cfm_gemm_swiglu(R, F, d, m->n.p, d, q13, m->act.p, F, s));
+    } else {
+      CK(gemm(m, R, 2 * F, d, m->n.p, d, b.w13, d, m->gu.p, 2 * F, 0.0f));
+      CK(cfm_swiglu(m->gu.p, R, F, m->act.p, s));
+    }
     CK(gemm(m, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
     if (i < split) CK(hipMemcpyAsync(m->skips[nsk++].p, xin, sizeof(float) * R * d, hipMemcpyDeviceToDevice, s));
   }

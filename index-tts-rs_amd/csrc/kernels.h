@@ -310,7 +310,11 @@ hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, lon
 // uint4 at out, rows padded to 64 and k to 128 with zeros), and the product over them:
 // the same values as cfm_gemm on W (K, lda multiples of 4, A 16-byte aligned).
 size_t cfm_split_weights_quads(int N, int K);
-hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s);
+hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s, int ilv = 0);
+// act [M][ldo] = silu(A W1^T) * (A W3^T) for the packed W = [w1; w3] (2F rows) split with
+// ilv = F: the SwiGLU in the product's epilogue (F a multiple of 32).
+hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const uint4 *Wp, float *act, int ldo,
+                           hipStream_t s);
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
                             float *y, int ldy, long sy, float beta, hipStream_t s);
 // The same product in fp32 FMAs for few rows (any M, any alignment; float4 loads when K,

@@ -458,14 +458,17 @@ struct GemmLds {
   uint16_t w[2][2][64 * 64];
 };
 
-// W [N][ldw] (k < K) -> the pre-split quads split_gemm_kernel<true> reads, zeros past N and K
-__global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int kp4, long n, uint4 *out) {
+// W [N][ldw] (k < K) -> the pre-split quads split_gemm_kernel<true> reads, zeros past N and K.
+// With ilv = F (N = 2F, the packed [w1; w3]), output row r holds input row (r >> 5 & 1) F +
+// 32 (r >> 6) + (r & 31): each 64-row tile is 32 rows of w1 then the matching 32 of w3.
+__global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int kp4, long n, int ilv, uint4 *out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int r = (int)(i / kp4), k = (int)(i % kp4) * 4;
+  const int src = ilv ? ((r >> 5) & 1) * ilv + 32 * (r >> 6) + (r & 31) : r;
   uint4 q = make_uint4(0u, 0u, 0u, 0u);
-  if (r < N && k < K) {
-    const float4 v = *reinterpret_cast<const float4 *>(W + (size_t)r * ldw + k);
+  if (src < N && k < K) {
+    const float4 v = *reinterpret_cast<const float4 *>(W + (size_t)src * ldw + k);
     split_f16x2(v.x, v.y, q.x, q.z);
     split_f16x2(v.z, v.w, q.y, q.w);
   }
@@ -475,7 +478,9 @@ __global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int 
 // PRE: W comes split already (cfm_split_weights): per row, 16 bytes per 4 values of k, {hi
 // (k, k+1), hi (k+2, k+3), lo (k, k+1), lo (k+2, k+3)}, wkp4 quads a row, rows padded to a
 // multiple of 64 and k to a multiple of 128 with zeros, copied to LDS as they are.
-template <bool PRE>
+// SWIGLU (with PRE, W split with ilv = F): tile columns 0-31 are w1 (gate) and 32-63 w3 (up)
+// outputs of the same 32 columns of act = silu(gate) * up, written to y [M][ldy] (beta 0).
+template <bool PRE, bool SWIGLU = false>
 __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const float *W, int ldw,
                                                          long sw, const uint4 *Wp, int wkp4, float *y, int ldy,
                                                          long sy, int M, int N, int K, float beta) {
@@ -574,6 +579,34 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
     for (int i = 0; i < 16; i++) red[i * 64] = acc[i];
   }
   __syncthreads();
+  if constexpr (SWIGLU) {
+    if (kg == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[i] += red[i * 64];
+    }
+    __syncthreads();  // every read of red done before the area is reused
+    float *up = reinterpret_cast<float *>(&sh.a[0][0][0]) + wm * 1024 + lane;
+    if (kg == 0 && wn == 1) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) up[i * 64] = acc[i];
+    }
+    __syncthreads();
+    if (kg == 0 && wn == 0) {
+      const int rb = m0 + wm * 32 + (lane >> 5) * 4, col = blockIdx.x * 32 + (lane & 31);
+      float o[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        o[i] = silu(acc[i]) * up[i * 64];
+        asm volatile("" : "+v"(o[i]));
+      }
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int r = rb + (i >> 2) * 8 + (i & 3);
+        if (r < M) y[(size_t)r * ldy + col] = o[i];
+      }
+    }
+    return;
+  }
   const int c = n0 + wn * 32 + (lane & 31);
   if (kg == 1 || c >= N) return;
 #pragma unroll
@@ -843,11 +876,21 @@ hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, lon
   return hipGetLastError();
 }
 size_t cfm_split_weights_quads(int N, int K) { return (size_t)((N + 63) / 64 * 64) * ((K + 127) / 128 * 32); }
-hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s) {
+hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s, int ilv) {
   if (N < 1 || K < 4 || K % 4 || ldw % 4 || ldw < K || (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
+  if (ilv && (ilv % 32 || N != 2 * ilv)) return hipErrorInvalidValue;
   const int kp4 = (K + 127) / 128 * 32;
   const long n = (long)((N + 63) / 64 * 64) * kp4;
-  hipLaunchKernelGGL(split_weights_kernel, dim3(nblk(n)), dim3(256), 0, s, W, ldw, N, K, kp4, n, out);
+  hipLaunchKernelGGL(split_weights_kernel, dim3(nblk(n)), dim3(256), 0, s, W, ldw, N, K, kp4, n, ilv, out);
+  return hipGetLastError();
+}
+hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const uint4 *Wp, float *act, int ldo,
+                           hipStream_t s) {
+  if (M < 1 || F < 32 || F % 32 || K < 4 || K % 4 || lda % 4 || ldo < F || (reinterpret_cast<uintptr_t>(A) & 15) ||
+      !Wp)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((split_gemm_kernel<true, true>), dim3(2 * F / 64, (M + 63) / 64, 1), dim3(512), 0, s, A, lda, 0L,
+                     nullptr, 0, 0L, Wp, (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f);
   return hipGetLastError();
 }
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
