@@ -72,7 +72,7 @@ struct Buf {
 };
 
 hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                int ldy, float beta);
+                int ldy, float beta, const float *bias = nullptr);
 
 struct Block {
   const float *wqkv, *wo, *w13, *w2, *skip_w, *skip_b, *an_w, *fn_w;
@@ -134,19 +134,19 @@ uint4 *split_weights(itts_cfm *m, const float *W, int ldw, int N, int K, int ilv
   return p;
 }
 
-// y[M][N] = A[M][K] W[N][K]^T + beta y (row-major; W rows ldw apart) on the estimator's
-// stream: row blocks of 64 and more on the split-fp16 MFMA GEMM over the weight's split
+// y[M][N] = A[M][K] W[N][K]^T (+ bias[n]) + beta y (row-major; W rows ldw apart) on the
+// estimator's stream: row blocks of 64 and more on the split-fp16 MFMA GEMM over the weight's split
 // quads, fewer rows (the per-batch timestep, AdaLN and WaveNet-conditioning projections,
 // forwards of under 64 frames) and operands the MFMA GEMM cannot take on the few-row fp32
 // product.
 hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                int ldy, float beta) {
+                int ldy, float beta, const float *bias) {
   if (M >= 64 && itts::cfm_gemm_fits(A, lda, W, ldw, K)) {
     const uint4 *wp = split_weights(m, W, ldw, N, K);
     if (!wp) return hipErrorOutOfMemory;
-    return itts::cfm_gemm_split_w(1, M, N, K, A, lda, 0, wp, y, ldy, 0, beta, m->s);
+    return itts::cfm_gemm_split_w(1, M, N, K, A, lda, 0, wp, y, ldy, 0, beta, m->s, bias);
   }
-  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, m->s);
+  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, m->s, bias);
 }
 
 itts_status check_config(const itts_cfm_config &c) {
@@ -202,11 +202,9 @@ itts_status timestep(itts_cfm *m, int e, int B, float *out) {
   const int d = m->c.dim;
   hipStream_t s = m->s;
   CK(cfm_temb(m->tdev.p, B, m->emb.p, s));
-  CK(cfm_bias_rows(m->th.p, d, m->te_b0[e], B, d, s));
-  CK(gemm(m, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 1.0f));
+  CK(gemm(m, B, d, kFreqDim, m->emb.p, kFreqDim, m->te_w0[e], kFreqDim, m->th.p, d, 0.0f, m->te_b0[e]));
   CK(cfm_silu(m->th.p, m->th.p, B * d, s));
-  CK(cfm_bias_rows(out, d, m->te_b2[e], B, d, s));
-  CK(gemm(m, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 1.0f));
+  CK(gemm(m, B, d, d, m->th.p, d, m->te_w2[e], d, out, d, 0.0f, m->te_b2[e]));
   return ITTS_OK;
 }
 
@@ -222,17 +220,13 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
   // conditioning vectors: t1, t2, every AdaLN's (w, b), WaveNet's per-layer g, FinalLayer's (shift, scale)
   if (itts_status st = timestep(m, 0, B, m->t1.p)) return st;
   if (itts_status st = timestep(m, 1, B, m->t2.p)) return st;
-  CK(cfm_bias_rows(m->mods.p, na2, m->ada_b, B, na2, s));
-  CK(gemm(m, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 1.0f));
-  CK(cfm_bias_rows(m->wng.p, 2 * d * NL, m->wc_b, B, 2 * d * NL, s));
-  CK(gemm(m, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 1.0f));
+  CK(gemm(m, B, na2, d, m->t1.p, d, m->ada_w, d, m->mods.p, na2, 0.0f, m->ada_b));
+  CK(gemm(m, B, 2 * d * NL, d, m->t2.p, d, m->wc_w, d, m->wng.p, 2 * d * NL, 0.0f, m->wc_b));
   CK(cfm_silu(m->t1.p, m->st.p, B * d, s));
-  CK(cfm_bias_rows(m->fmod.p, 2 * d, m->fa_b, B, 2 * d, s));
-  CK(gemm(m, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 1.0f));
+  CK(gemm(m, B, 2 * d, d, m->st.p, d, m->fa_w, d, m->fmod.p, 2 * d, 0.0f, m->fa_b));
   // h = cond_x_merge_linear(x_merged)
   float *cur = m->hA.p, *oth = m->hB.p;
-  CK(cfm_bias_rows(cur, d, m->merge_b, R, d, s));
-  CK(gemm(m, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 1.0f));
+  CK(gemm(m, R, d, MD, merged, MD, m->merge_w, MD, cur, d, 0.0f, m->merge_b));
   // U-ViT blocks with long skips (cfm.rs:553-563)
   int nsk = 0;
   for (int i = 0; i < Lc; i++) {
@@ -240,8 +234,7 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     float *xin = cur;
     if (i > split && nsk > 0) {  // skip_in_linear([h, skip]) as two accumulating GEMMs
       const float *sk = m->skips[--nsk].p;
-      CK(cfm_bias_rows(oth, d, b.skip_b, R, d, s));
-      CK(gemm(m, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 1.0f));
+      CK(gemm(m, R, d, d, cur, d, b.skip_w, 2 * d, oth, d, 0.0f, b.skip_b));
       CK(gemm(m, R, d, d, sk, d, b.skip_w + d, 2 * d, oth, d, 1.0f));
       xin = oth;
       oth = cur;
@@ -268,11 +261,9 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
   }
   // transformer.norm, x_res = skip_linear([h, x_t]), h = conv1(x_res)
   CK(cfm_adaln(cur, m->n.p, R, T, d, m->mods.p + (size_t)(2 * Lc) * 2 * d, na2, m->tn_w, s));
-  CK(cfm_bias_rows(m->xres.p, d, m->skl_b, R, d, s));
-  CK(gemm(m, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 1.0f));
+  CK(gemm(m, R, d, d, m->n.p, d, m->skl_w, d + C, m->xres.p, d, 0.0f, m->skl_b));
   CK(gemm(m, R, d, C, x_t, C, m->skl_w + d, d + C, m->xres.p, d, 1.0f));
-  CK(cfm_bias_rows(oth, d, m->c1_b, R, d, s));
-  CK(gemm(m, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 1.0f));
+  CK(gemm(m, R, d, d, m->xres.p, d, m->c1_w, d, oth, d, 0.0f, m->c1_b));
   // WaveNet (cfm.rs:373-408): h in a zero-padded [B][T + 2 pad][d] buffer
   CK(cfm_pad_rows(oth, B, T, d, pad, m->hpad.p, s));
   CK(hipMemsetAsync(m->oacc.p, 0, sizeof(float) * R * d, s));
@@ -294,10 +285,8 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
   CK(cfm_add_bias(m->oacc.p, d, m->rp_b, R, d, s));
   CK(gemm(m, R, d, d, m->xres.p, d, m->rp_w, d, m->oacc.p, d, 1.0f));
   CK(cfm_final_norm(m->oacc.p, m->n.p, R, T, d, m->fmod.p, s));
-  CK(cfm_bias_rows(cur, d, m->fl_b, R, d, s));
-  CK(gemm(m, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 1.0f));
-  CK(cfm_bias_rows(m->v.p, C, m->c2_b, R, C, s));
-  CK(gemm(m, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 1.0f));
+  CK(gemm(m, R, d, d, m->n.p, d, m->fl_w, d, cur, d, 0.0f, m->fl_b));
+  CK(gemm(m, R, C, d, cur, d, m->c2_w, d, m->v.p, C, 0.0f, m->c2_b));
   return ITTS_OK;
 }
 

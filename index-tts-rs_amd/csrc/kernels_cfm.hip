@@ -483,7 +483,8 @@ __global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int 
 template <bool PRE, bool SWIGLU = false>
 __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const float *W, int ldw,
                                                          long sw, const uint4 *Wp, int wkp4, float *y, int ldy,
-                                                         long sy, int M, int N, int K, float beta) {
+                                                         long sy, int M, int N, int K, float beta,
+                                                         const float *bias) {
   __shared__ GemmLds sh;
   const int tid = threadIdx.x, lane = tid & 63, wv = (tid >> 6) & 3, kg = tid >> 8, wm = wv >> 1, wn = wv & 1;
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
@@ -611,6 +612,11 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   if (kg == 1 || c >= N) return;
 #pragma unroll
   for (int i = 0; i < 16; i++) acc[i] += red[i * 64];
+  if (bias) {
+    const float bc = bias[c];
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = acc[i] + bc;
+  }
   // With beta, the old outputs are loaded together (rows clamped, not predicated) and the
   // new values formed before the row-predicated stores: read and written element by
   // element, each load would wait behind the previous element's store.
@@ -737,7 +743,8 @@ __global__ void pad_rows_kernel(const float *x, int B, int T, int d, int pad, fl
 template <int MT, int VEC>
 __global__ __launch_bounds__(256) void rows_gemm_kernel(const float *__restrict__ A, int lda, long sa,
                                                         const float *__restrict__ W, int ldw, long sw, float *y,
-                                                        int ldy, long sy, int M, int N, int K, float beta) {
+                                                        int ldy, long sy, int M, int N, int K, float beta,
+                                                        const float *bias) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -776,6 +783,7 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const float *__restrict_
     for (int j = 1; j < MT; j++)
       if (lane == j) v = acc[j];
     float *dst = y + z * sy + (size_t)(m0 + lane) * ldy + n;
+    if (bias) v = v + bias[n];
     *dst = beta != 0.0f ? v + beta * *dst : v;
   }
 }
@@ -872,7 +880,7 @@ hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, lon
                     float *y, int ldy, long sy, float beta, hipStream_t s) {
   if (batch < 1 || M < 1 || N < 1 || K < 1 || !cfm_gemm_fits(A, lda, W, ldw, K)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_gemm_kernel<false>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
-                     W, ldw, sw, nullptr, 0, y, ldy, sy, M, N, K, beta);
+                     W, ldw, sw, nullptr, 0, y, ldy, sy, M, N, K, beta, nullptr);
   return hipGetLastError();
 }
 size_t cfm_split_weights_quads(int N, int K) { return (size_t)((N + 63) / 64 * 64) * ((K + 127) / 128 * 32); }
@@ -890,25 +898,25 @@ hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const u
       !Wp)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL((split_gemm_kernel<true, true>), dim3(2 * F / 64, (M + 63) / 64, 1), dim3(512), 0, s, A, lda, 0L,
-                     nullptr, 0, 0L, Wp, (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f);
+                     nullptr, 0, 0L, Wp, (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f, nullptr);
   return hipGetLastError();
 }
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
-                            float *y, int ldy, long sy, float beta, hipStream_t s) {
+                            float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias) {
   if (batch < 1 || M < 1 || N < 1 || K < 4 || K % 4 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || !Wp)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_gemm_kernel<true>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
-                     nullptr, 0, 0, Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta);
+                     nullptr, 0, 0, Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta, bias);
   return hipGetLastError();
 }
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
-                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s) {
+                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias) {
   if (batch < 1 || M < 1 || N < 1 || K < 1 || lda < K || ldw < K || ldy < N) return hipErrorInvalidValue;
   const bool v4 = K % 4 == 0 && lda % 4 == 0 && ldw % 4 == 0 && sa % 4 == 0 && sw % 4 == 0 &&
                   (reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0;
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const dim3 grid((N + 3) / 4, (M + mt - 1) / mt, batch);
-#define ROWS_GEMM(MT, VEC)                                                                                        hipLaunchKernelGGL((rows_gemm_kernel<MT, VEC>), grid, dim3(256), 0, s, A, lda, sa, W, ldw, sw, y, ldy, sy, M, N,                      K, beta)
+#define ROWS_GEMM(MT, VEC)                                                                                        hipLaunchKernelGGL((rows_gemm_kernel<MT, VEC>), grid, dim3(256), 0, s, A, lda, sa, W, ldw, sw, y, ldy, sy, M, N,                      K, beta, bias)
   if (v4) {
     if (mt == 1) ROWS_GEMM(1, 4);
     else if (mt == 2) ROWS_GEMM(2, 4);
