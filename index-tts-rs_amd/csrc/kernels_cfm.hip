@@ -434,7 +434,7 @@ __global__ void attn_combine_kernel(const float *part_o, const float *part_ml, i
 #pragma unroll
   for (int s = 0; s < kMaxSplits; s++)
     if (s < S) {
-      const float f = mv[s] == -INFINITY ? 0.0f : expf(mv[s] - M);
+      const float f = mv[s] == -INFINITY ? 0.0f : __expf(mv[s] - M);
       num += ov[s] * f;
       den += lv[s] * f;
     }
