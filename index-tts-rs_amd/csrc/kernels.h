@@ -299,16 +299,14 @@ int cfm_attn_splits(int B, int T, int H, int n_cu);
 // kv_split: workspace of cfm_kv_split_halves(B, T, H) 16-bit values (K with rope and V as
 // fp16 hi/lo planes, built once per call and shared by every query tile).
 int cfm_kv_split_halves(int B, int T, int H);
-// y[z] = A[z] W[z]^T + beta y[z] for z < batch (row-major; A rows lda apart and allowed to
-// overlap, W rows ldw apart, batch strides sa / sw / sy in floats) on the MFMA units with fp16
-// hi/lo operands and fp32 accumulation.  cfm_gemm_fits: K, lda, ldw multiples of 4 and A, W
-// 16-byte aligned (the launch rejects anything else).
+// The MFMA GEMM's operand rules: K, lda, ldw multiples of 4 and A, W 16-byte aligned (the
+// split and the launches reject anything else).
 bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K);
-hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
-                    float *y, int ldy, long sy, float beta, hipStream_t s);
-// The constant operand W split once into fp16 hi/lo quads (cfm_split_weights_quads(N, K)
-// uint4 at out, rows padded to 64 and k to 128 with zeros), and the product over them:
-// the same values as cfm_gemm on W (K, lda multiples of 4, A 16-byte aligned).
+// The constant operand W [N][ldw] split once into fp16 hi/lo quads (cfm_split_weights_quads(N,
+// K) uint4 at out, rows padded to 64 and k to 128 with zeros), and the products over them:
+// cfm_gemm_split_w y[z] = A[z] W^T (+ bias) + beta y[z] for z < batch (row-major; A rows lda
+// apart and allowed to overlap, batch strides sa / sy in floats) on the MFMA units with fp16
+// hi/lo operands and fp32 accumulation (K, lda multiples of 4, A 16-byte aligned).
 size_t cfm_split_weights_quads(int N, int K);
 hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s, int ilv = 0);
 // act [M][ldo] = silu(A W1^T) * (A W3^T) for the packed W = [w1; w3] (2F rows) split with

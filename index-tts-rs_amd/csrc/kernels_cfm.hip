@@ -475,21 +475,19 @@ __global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int 
   out[i] = q;
 }
 
-// PRE: W comes split already (cfm_split_weights): per row, 16 bytes per 4 values of k, {hi
-// (k, k+1), hi (k+2, k+3), lo (k, k+1), lo (k+2, k+3)}, wkp4 quads a row, rows padded to a
+// W comes split already (cfm_split_weights): per row, 16 bytes per 4 values of k, {hi (k,
+// k+1), hi (k+2, k+3), lo (k, k+1), lo (k+2, k+3)}, wkp4 quads a row, rows padded to a
 // multiple of 64 and k to a multiple of 128 with zeros, copied to LDS as they are.
-// SWIGLU (with PRE, W split with ilv = F): tile columns 0-31 are w1 (gate) and 32-63 w3 (up)
-// outputs of the same 32 columns of act = silu(gate) * up, written to y [M][ldy] (beta 0).
-template <bool PRE, bool SWIGLU = false>
-__global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const float *W, int ldw,
-                                                         long sw, const uint4 *Wp, int wkp4, float *y, int ldy,
-                                                         long sy, int M, int N, int K, float beta,
+// SWIGLU (W split with ilv = F): tile columns 0-31 are w1 (gate) and 32-63 w3 (up) outputs
+// of the same 32 columns of act = silu(gate) * up, written to y [M][ldy] (beta 0).
+template <bool SWIGLU = false>
+__global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const uint4 *Wp, int wkp4,
+                                                         float *y, int ldy, long sy, int M, int N, int K, float beta,
                                                          const float *bias) {
   __shared__ GemmLds sh;
   const int tid = threadIdx.x, lane = tid & 63, wv = (tid >> 6) & 3, kg = tid >> 8, wm = wv >> 1, wn = wv & 1;
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
   A += blockIdx.z * sa;
-  W += blockIdx.z * sw;
   y += blockIdx.z * sy;
   // K tiles of 64, rounded up to a pair (a tile past K is split as zeros), so that the
   // loop below runs whole pairs with no conditional step or store
@@ -499,20 +497,16 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   // barrier rather than being the next thing waited for (one set: each K tile cost about
   // one load latency).  The loads are unpredicated, with the row and k indexes clamped
   // into the operands (so that the compiler's wait counting keeps the later set in
-  // flight).  Rows past M or N are loaded as a copy of the last row: they reach only output
-  // rows and columns that are not stored.  Values past K are zeroed in W's planes (A's
-  // clamped values there are finite, so the products vanish).
+  // flight).  Rows past M are loaded as a copy of the last row: they reach only output rows
+  // that are not stored.  Values past K are zeros in W's planes (A's clamped values there
+  // are finite, so the products vanish).
   float4 ra[2][2], rw[2][2];
   auto load = [&](int kt, float4(&a4)[2], float4(&w4)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int idx = tid + 512 * j, row = idx >> 4, k = min(kt * 64 + (idx & 15) * 4, K - 4);
       a4[j] = *reinterpret_cast<const float4 *>(A + (size_t)min(m0 + row, M - 1) * lda + k);
-      if constexpr (PRE) {
-        w4[j] = __builtin_bit_cast(float4, Wp[(size_t)(n0 + row) * wkp4 + kt * 16 + (idx & 15)]);
-      } else {
-        w4[j] = *reinterpret_cast<const float4 *>(W + (size_t)min(n0 + row, N - 1) * ldw + k);
-      }
+      w4[j] = __builtin_bit_cast(float4, Wp[(size_t)(n0 + row) * wkp4 + kt * 16 + (idx & 15)]);
     }
   };
   auto store = [&](int buf, int kt, const float4(&a4)[2], const float4(&w4)[2]) __attribute__((always_inline)) {
@@ -520,19 +514,12 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
     for (int j = 0; j < 2; j++) {
       const int idx = tid + 512 * j, row = idx >> 4, c4 = idx & 15;
       const int off = swz(row, c4 >> 1) + (c4 & 1) * 4;
-      const bool kin = kt * 64 + c4 * 4 < K;
       const float4 av = a4[j];
-      uint32_t ah0, al0, ah1, al1, wh0, wl0, wh1, wl1;
+      uint32_t ah0, al0, ah1, al1;
       split_f16x2(av.x, av.y, ah0, al0);
       split_f16x2(av.z, av.w, ah1, al1);
-      if constexpr (PRE) {
-        const uint4 q = __builtin_bit_cast(uint4, w4[j]);
-        wh0 = q.x, wh1 = q.y, wl0 = q.z, wl1 = q.w;
-      } else {
-        const float4 wv4 = kin ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        split_f16x2(wv4.x, wv4.y, wh0, wl0);
-        split_f16x2(wv4.z, wv4.w, wh1, wl1);
-      }
+      const uint4 q = __builtin_bit_cast(uint4, w4[j]);
+      const uint32_t wh0 = q.x, wh1 = q.y, wl0 = q.z, wl1 = q.w;
       *reinterpret_cast<uint2 *>(&sh.a[buf][0][off]) = make_uint2(ah0, ah1);
       *reinterpret_cast<uint2 *>(&sh.a[buf][1][off]) = make_uint2(al0, al1);
       *reinterpret_cast<uint2 *>(&sh.w[buf][0][off]) = make_uint2(wh0, wh1);
@@ -876,13 +863,6 @@ bool cfm_gemm_fits(const float *A, int lda, const float *W, int ldw, int K) {
   return K % 4 == 0 && lda % 4 == 0 && ldw % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
 }
-hipError_t cfm_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw, long sw,
-                    float *y, int ldy, long sy, float beta, hipStream_t s) {
-  if (batch < 1 || M < 1 || N < 1 || K < 1 || !cfm_gemm_fits(A, lda, W, ldw, K)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_gemm_kernel<false>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
-                     W, ldw, sw, nullptr, 0, y, ldy, sy, M, N, K, beta, nullptr);
-  return hipGetLastError();
-}
 size_t cfm_split_weights_quads(int N, int K) { return (size_t)((N + 63) / 64 * 64) * ((K + 127) / 128 * 32); }
 hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, hipStream_t s, int ilv) {
   if (N < 1 || K < 4 || K % 4 || ldw % 4 || ldw < K || (reinterpret_cast<uintptr_t>(W) & 15)) return hipErrorInvalidValue;
@@ -897,16 +877,16 @@ hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const u
   if (M < 1 || F < 32 || F % 32 || K < 4 || K % 4 || lda % 4 || ldo < F || (reinterpret_cast<uintptr_t>(A) & 15) ||
       !Wp)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((split_gemm_kernel<true, true>), dim3(2 * F / 64, (M + 63) / 64, 1), dim3(512), 0, s, A, lda, 0L,
-                     nullptr, 0, 0L, Wp, (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f, nullptr);
+  hipLaunchKernelGGL(split_gemm_kernel<true>, dim3(2 * F / 64, (M + 63) / 64, 1), dim3(512), 0, s, A, lda, 0L, Wp,
+                     (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f, nullptr);
   return hipGetLastError();
 }
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
                             float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias) {
   if (batch < 1 || M < 1 || N < 1 || K < 4 || K % 4 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || !Wp)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_gemm_kernel<true>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
-                     nullptr, 0, 0, Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta, bias);
+  hipLaunchKernelGGL(split_gemm_kernel<false>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
+                     Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta, bias);
   return hipGetLastError();
 }
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
