@@ -89,22 +89,29 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(const float *x, float *
   if (r >= R) return;  // whole waves leave together
   const int b = r / T;
   const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)r * d);
-  float4 v[NV];
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NV; j++) {
-    v[j] = xr[64 * j + lane];
-    s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
-  }
-  const float rs = 1.0f / sqrtf(wave64_sum_dpp(s) / (float)d + 1e-5f);
   const float4 *w = reinterpret_cast<const float4 *>(mod + (size_t)b * ld_mod);
   const float4 *bb = reinterpret_cast<const float4 *>(mod + (size_t)b * ld_mod + d);
   const float4 *nw = reinterpret_cast<const float4 *>(norm_w);
+  // the row, its batch's modulation and the norm weight all loaded before the reduction
+  // (one memory round trip, not two)
+  float4 v[NV], wv[NV], bv[NV], nv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int c = 64 * j + lane;
+    v[j] = xr[c];
+    wv[j] = w[c];
+    bv[j] = bb[c];
+    nv[j] = nw[c];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; j++) s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+  const float rs = 1.0f / sqrtf(wave64_sum_dpp(s) / (float)d + 1e-5f);
   float4 *yr = reinterpret_cast<float4 *>(y + (size_t)r * d);
 #pragma unroll
   for (int j = 0; j < NV; j++) {
     const int c = 64 * j + lane;
-    const float4 wj = w[c], bj = bb[c], nj = nw[c];
+    const float4 wj = wv[j], bj = bv[j], nj = nv[j];
     yr[c] = make_float4(wj.x * (v[j].x * rs * nj.x) + bj.x, wj.y * (v[j].y * rs * nj.y) + bj.y,
                         wj.z * (v[j].z * rs * nj.z) + bj.z, wj.w * (v[j].w * rs * nj.w) + bj.w);
   }
