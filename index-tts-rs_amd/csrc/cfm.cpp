@@ -72,7 +72,7 @@ struct Buf {
 };
 
 hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                int ldy, float beta, const float *bias = nullptr);
+                int ldy, float beta, const float *bias = nullptr, const float *yr = nullptr);
 
 struct Block {
   const float *wqkv, *wo, *w13, *w2, *skip_w, *skip_b, *an_w, *fn_w;
@@ -140,13 +140,13 @@ uint4 *split_weights(itts_cfm *m, const float *W, int ldw, int N, int K, int ilv
 // forwards of under 64 frames) and operands the MFMA GEMM cannot take on the few-row fp32
 // product.
 hipError_t gemm(itts_cfm *m, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *y,
-                int ldy, float beta, const float *bias) {
+                int ldy, float beta, const float *bias, const float *yr) {
   if (M >= 64 && itts::cfm_gemm_fits(A, lda, W, ldw, K)) {
     const uint4 *wp = split_weights(m, W, ldw, N, K);
     if (!wp) return hipErrorOutOfMemory;
-    return itts::cfm_gemm_split_w(1, M, N, K, A, lda, 0, wp, y, ldy, 0, beta, m->s, bias);
+    return itts::cfm_gemm_split_w(1, M, N, K, A, lda, 0, wp, y, ldy, 0, beta, m->s, bias, yr);
   }
-  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, m->s, bias);
+  return itts::cfm_rows_gemm(1, M, N, K, A, lda, 0, W, ldw, 0, y, ldy, 0, beta, m->s, bias, yr);
 }
 
 itts_status check_config(const itts_cfm_config &c) {
@@ -245,7 +245,16 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
     CK(gemm(m, R, 3 * d, d, m->n.p, d, b.wqkv, d, m->qkv.p, 3 * d, 0.0f));
     CK(cfm_attention(m->qkv.p, m->rope.p, B, T, d, c.n_heads, m->att.p, m->apo.p, m->aml.p,
                      reinterpret_cast<uint16_t *>(m->kvs.p), m->n_cu, s));
-    CK(gemm(m, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));  // hidden = x_in + attn
+    // hidden = x_in + attn: in place, except where x_in must be kept (a block of the first
+    // half writes its output straight into its long-skip stash; the middle block's input
+    // is the last stash) and the sum goes out of place
+    if (i <= split) {
+      float *dst = i < split ? m->skips[nsk].p : (cur == m->hA.p ? m->hB.p : m->hA.p);
+      CK(gemm(m, R, d, d, m->att.p, d, b.wo, d, dst, d, 1.0f, nullptr, xin));
+      xin = dst;
+    } else {
+      CK(gemm(m, R, d, d, m->att.p, d, b.wo, d, xin, d, 1.0f));
+    }
     CK(cfm_adaln(xin, m->n.p, R, T, d, mod_f, na2, b.fn_w, s));
     if (R >= 64 && F % 32 == 0 && cfm_gemm_fits(m->n.p, d, b.w13, d, d)) {
       // the SwiGLU in the [w1; w3] product's epilogue, over rows interleaved per 32
@@ -257,7 +266,11 @@ itts_status forward(itts_cfm *m, const float *x_t, const float *merged, int B, i
       CK(cfm_swiglu(m->gu.p, R, F, m->act.p, s));
     }
     CK(gemm(m, R, d, F, m->act.p, F, b.w2, F, xin, d, 1.0f));  // hidden + ffn
-    if (i < split) CK(hipMemcpyAsync(m->skips[nsk++].p, xin, sizeof(float) * R * d, hipMemcpyDeviceToDevice, s));
+    if (i < split) nsk++;
+    if (i <= split) {  // the block's output, in its stash or in the scratch buffer that is not cur
+      if (i == split) oth = cur == m->hA.p || cur == m->hB.p ? cur : (xin == m->hA.p ? m->hB.p : m->hA.p);
+      cur = xin;
+    }
   }
   // transformer.norm, x_res = skip_linear([h, x_t]), h = conv1(x_res)
   CK(cfm_adaln(cur, m->n.p, R, T, d, m->mods.p + (size_t)(2 * Lc) * 2 * d, na2, m->tn_w, s));

@@ -314,12 +314,15 @@ hipError_t cfm_split_weights(const float *W, int ldw, int N, int K, uint4 *out, 
 hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const uint4 *Wp, float *act, int ldo,
                            hipStream_t s);
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
-                            float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias = nullptr);
+                            float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias = nullptr,
+                            const float *yr = nullptr);
 // The same product in fp32 FMAs for few rows (any M, any alignment; float4 loads when K,
 // lda, ldw, sa, sw are multiples of 4 and A, W are 16-byte aligned); beta 0 never reads y.
-// With bias (here and in cfm_gemm_split_w): y = A W^T + bias[n] + beta y.
+// With bias (here and in cfm_gemm_split_w): y = A W^T + bias[n] + beta y; with yr, beta's
+// old values come from yr (same layout as y) and y is written out of place.
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
-                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias = nullptr);
+                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias = nullptr,
+                         const float *yr = nullptr);
 hipError_t cfm_attention(const float *qkv, const float *rope_tab, int B, int T, int d, int H, float *out,
                          float *part_o, float *part_ml, uint16_t *kv_split, int n_cu, hipStream_t s);
 hipError_t cfm_swiglu(const float *gu, int R, int F, float *out, hipStream_t s);

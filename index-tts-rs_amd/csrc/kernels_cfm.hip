@@ -490,12 +490,13 @@ __global__ void split_weights_kernel(const float *W, int ldw, int N, int K, int 
 template <bool SWIGLU = false>
 __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda, long sa, const uint4 *Wp, int wkp4,
                                                          float *y, int ldy, long sy, int M, int N, int K, float beta,
-                                                         const float *bias) {
+                                                         const float *bias, const float *yr) {
   __shared__ GemmLds sh;
   const int tid = threadIdx.x, lane = tid & 63, wv = (tid >> 6) & 3, kg = tid >> 8, wm = wv >> 1, wn = wv & 1;
   const int n0 = blockIdx.x * 64, m0 = blockIdx.y * 64;
   A += blockIdx.z * sa;
   y += blockIdx.z * sy;
+  const float *ysrc = yr ? yr + blockIdx.z * sy : y;  // beta's old values (y itself unless given)
   // K tiles of 64, rounded up to a pair (a tile past K is split as zeros), so that the
   // loop below runs whole pairs with no conditional step or store
   const int nk = (K + 127) / 128 * 2;
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(512) void split_gemm_kernel(const float *A, int lda
   if (beta != 0.0f) {
     float old[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) old[i] = y[(size_t)min(rb + (i >> 2) * 8 + (i & 3), M - 1) * ldy + c];
+    for (int i = 0; i < 16; i++) old[i] = ysrc[(size_t)min(rb + (i >> 2) * 8 + (i & 3), M - 1) * ldy + c];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       acc[i] = acc[i] + beta * old[i];
@@ -738,7 +739,7 @@ template <int MT, int VEC>
 __global__ __launch_bounds__(256) void rows_gemm_kernel(const float *__restrict__ A, int lda, long sa,
                                                         const float *__restrict__ W, int ldw, long sw, float *y,
                                                         int ldy, long sy, int M, int N, int K, float beta,
-                                                        const float *bias) {
+                                                        const float *bias, const float *yr) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -777,8 +778,9 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const float *__restrict_
     for (int j = 1; j < MT; j++)
       if (lane == j) v = acc[j];
     float *dst = y + z * sy + (size_t)(m0 + lane) * ldy + n;
+    const float *src = yr ? yr + z * sy + (size_t)(m0 + lane) * ldy + n : dst;
     if (bias) v = v + bias[n];
-    *dst = beta != 0.0f ? v + beta * *dst : v;
+    *dst = beta != 0.0f ? v + beta * *src : v;
   }
 }
 
@@ -885,25 +887,27 @@ hipError_t cfm_gemm_swiglu(int M, int F, int K, const float *A, int lda, const u
       !Wp)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_gemm_kernel<true>, dim3(2 * F / 64, (M + 63) / 64, 1), dim3(512), 0, s, A, lda, 0L, Wp,
-                     (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f, nullptr);
+                     (K + 127) / 128 * 32, act, ldo, 0L, M, 2 * F, K, 0.0f, nullptr, nullptr);
   return hipGetLastError();
 }
 hipError_t cfm_gemm_split_w(int batch, int M, int N, int K, const float *A, int lda, long sa, const uint4 *Wp,
-                            float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias) {
+                            float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias,
+                            const float *yr) {
   if (batch < 1 || M < 1 || N < 1 || K < 4 || K % 4 || lda % 4 || (reinterpret_cast<uintptr_t>(A) & 15) || !Wp)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_gemm_kernel<false>, dim3((N + 63) / 64, (M + 63) / 64, batch), dim3(512), 0, s, A, lda, sa,
-                     Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta, bias);
+                     Wp, (K + 127) / 128 * 32, y, ldy, sy, M, N, K, beta, bias, yr);
   return hipGetLastError();
 }
 hipError_t cfm_rows_gemm(int batch, int M, int N, int K, const float *A, int lda, long sa, const float *W, int ldw,
-                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias) {
+                         long sw, float *y, int ldy, long sy, float beta, hipStream_t s, const float *bias,
+                         const float *yr) {
   if (batch < 1 || M < 1 || N < 1 || K < 1 || lda < K || ldw < K || ldy < N) return hipErrorInvalidValue;
   const bool v4 = K % 4 == 0 && lda % 4 == 0 && ldw % 4 == 0 && sa % 4 == 0 && sw % 4 == 0 &&
                   (reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(W) & 15) == 0;
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const dim3 grid((N + 3) / 4, (M + mt - 1) / mt, batch);
-#define ROWS_GEMM(MT, VEC)                                                                                        hipLaunchKernelGGL((rows_gemm_kernel<MT, VEC>), grid, dim3(256), 0, s, A, lda, sa, W, ldw, sw, y, ldy, sy, M, N,                      K, beta, bias)
+#define ROWS_GEMM(MT, VEC)                                                                                        hipLaunchKernelGGL((rows_gemm_kernel<MT, VEC>), grid, dim3(256), 0, s, A, lda, sa, W, ldw, sw, y, ldy, sy, M, N,                      K, beta, bias, yr)
   if (v4) {
     if (mt == 1) ROWS_GEMM(1, 4);
     else if (mt == 2) ROWS_GEMM(2, 4);
